@@ -1,0 +1,207 @@
+"""Python binding of libgemma4_kv.so, the MI355X build of gemma.c's KV-cache
+path (paged K/V append, split-K decode attention, prefill-chunk attention).
+
+This module is a thin ctypes layer over the C-ABI declared in include/*.h; it
+mirrors the reference's C++ entry points (same names, argument order and
+hipError_t return codes) so tests read like the reference's own tests.
+Device buffers are torch tensors (PyTorch supplies device memory and the
+stream); nothing here computes on the host. If the shared library is missing
+the import of any entry point raises: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libgemma4_kv.so"
+
+HIP_SUCCESS = 0
+HIP_ERROR_INVALID_VALUE = 1
+
+QUERY_HEADS = 16
+
+
+class Gemma4KvCacheConfig(ctypes.Structure):
+    """Same 8 x int32 layout as the reference struct (src/gemma4_kv_cache.cuh:9-18)."""
+
+    _fields_ = [
+        ("num_layers", ctypes.c_int32),
+        ("num_pages", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("max_pages_per_seq", ctypes.c_int32),
+        ("batch_size", ctypes.c_int32),
+        ("num_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("window_size", ctypes.c_int32),
+    ]
+
+    def as_tuple(self):
+        return tuple(getattr(self, f) for f, _ in self._fields_)
+
+    def __repr__(self) -> str:
+        return "Gemma4KvCacheConfig(%s)" % ", ".join(
+            f"{f}={getattr(self, f)}" for f, _ in self._fields_)
+
+
+def make_config(num_layers, num_pages, page_size, max_pages_per_seq, batch_size,
+                num_heads, head_dim, window_size) -> Gemma4KvCacheConfig:
+    return Gemma4KvCacheConfig(num_layers, num_pages, page_size, max_pages_per_seq,
+                               batch_size, num_heads, head_dim, window_size)
+
+
+class HipError(RuntimeError):
+    def __init__(self, code: int, what: str):
+        super().__init__(f"{what} returned hipError_t {code}")
+        self.code = code
+
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_F32 = ctypes.c_float
+_CFG = Gemma4KvCacheConfig
+
+# name -> (restype, argtypes); every symbol include/*.h declares with C linkage.
+SIGNATURES = {
+    "gemma4_kv_cache_make_config": (_CFG, [ctypes.c_bool, _I32, _I32, _I32]),
+    "gemma4_kv_cache_layer_index": (_I32, [_I32, ctypes.c_bool]),
+    "gemma4_kv_cache_ensure_page_ptr": (_I32, [_P, _P, _I64, ctypes.POINTER(_CFG), _I32, _I32]),
+    "gemma4_kv_cache_ensure_range_ptr": (_I32, [_P, _P, _I64, ctypes.POINTER(_CFG), _I32, _I32, _I32]),
+    "gemma4_kv_cache_write_bf16": (_I32, [_P, _P, _CFG, _P, _P, _P, _I32, _I32, _P, _P, _P]),
+    "gemma4_kv_cache_write_prefill_bf16": (_I32, [_P, _P, _CFG, _P, _P, _P, _I32, _I32, _I32, _P, _P, _P]),
+    "gemma4_flash_attention_decode_paged_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
+    "gemma4_flash_attention_append_decode_paged_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
+    "gemma4_decode_split_plan": (_I32, [_CFG, _I32, _I32, _I32, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
+}
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load the in-tree shared library (after torch, so both share one HIP runtime)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise ImportError(
+            f"{LIB_PATH} is not built; run gemma_kv.build.build() (or __graft_entry__.build())")
+    try:
+        import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+    except ImportError:
+        pass
+    handle = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = handle
+    return handle
+
+
+def ptr(x) -> int:
+    """Device/host address of a tensor, an int, or None (null)."""
+    if x is None:
+        return 0
+    if isinstance(x, int):
+        return x
+    return x.data_ptr()
+
+
+def stream_handle(stream=None) -> int:
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def check(code: int, what: str = "call") -> None:
+    if code != HIP_SUCCESS:
+        raise HipError(code, what)
+
+
+# ---- host helpers (no device work) ---------------------------------------
+
+def kv_cache_make_config(global_cache: bool, num_pages: int, page_size: int,
+                         max_pages_per_seq: int) -> Gemma4KvCacheConfig:
+    return lib().gemma4_kv_cache_make_config(bool(global_cache), num_pages, page_size,
+                                             max_pages_per_seq)
+
+
+def kv_cache_layer_index(model_layer: int, global_cache: bool) -> int:
+    return lib().gemma4_kv_cache_layer_index(model_layer, bool(global_cache))
+
+
+def kv_cache_ensure_page(page_table, slot_logical_pages, config, batch, position) -> int:
+    """page_table / slot_logical_pages: int32 numpy arrays, mutated in place."""
+    assert page_table.dtype.name == "int32" and slot_logical_pages.dtype.name == "int32"
+    n = min(page_table.size, slot_logical_pages.size)
+    return lib().gemma4_kv_cache_ensure_page_ptr(
+        page_table.ctypes.data, slot_logical_pages.ctypes.data, n,
+        ctypes.byref(config), batch, position)
+
+
+def kv_cache_ensure_range(page_table, slot_logical_pages, config, batch,
+                          first_position, token_count) -> int:
+    assert page_table.dtype.name == "int32" and slot_logical_pages.dtype.name == "int32"
+    n = min(page_table.size, slot_logical_pages.size)
+    return lib().gemma4_kv_cache_ensure_range_ptr(
+        page_table.ctypes.data, slot_logical_pages.ctypes.data, n,
+        ctypes.byref(config), batch, first_position, token_count)
+
+
+def decode_split_plan(config, batch_count: int, max_live_keys: int,
+                      target_workgroups: int = 0):
+    s = _I32()
+    n = _I32()
+    check(lib().gemma4_decode_split_plan(config, batch_count, max_live_keys,
+                                         target_workgroups, ctypes.byref(s),
+                                         ctypes.byref(n)), "gemma4_decode_split_plan")
+    return s.value, n.value
+
+
+# ---- device entry points (return hipError_t codes, like the reference) ----
+
+def kv_cache_write_bf16(cache_k, cache_v, config, page_table, token_batch,
+                        token_position, token_count, layer, k, v, stream=None) -> int:
+    return lib().gemma4_kv_cache_write_bf16(
+        ptr(cache_k), ptr(cache_v), config, ptr(page_table), ptr(token_batch),
+        ptr(token_position), token_count, layer, ptr(k), ptr(v), stream_handle(stream))
+
+
+def kv_cache_write_prefill_bf16(cache_k, cache_v, config, page_table, token_batch,
+                                token_position, batch_size, seq_len, layer, k, v,
+                                stream=None) -> int:
+    return lib().gemma4_kv_cache_write_prefill_bf16(
+        ptr(cache_k), ptr(cache_v), config, ptr(page_table), ptr(token_batch),
+        ptr(token_position), batch_size, seq_len, layer, ptr(k), ptr(v),
+        stream_handle(stream))
+
+
+def flash_attention_decode_paged_bf16(out, partial_m, partial_l, partial_acc, q,
+                                      cache_k, cache_v, page_table, seq_lengths,
+                                      config, layer, softmax_scale, split_size,
+                                      num_splits, batch_count, stream=None) -> int:
+    return lib().gemma4_flash_attention_decode_paged_bf16(
+        ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(q),
+        ptr(cache_k), ptr(cache_v), ptr(page_table), ptr(seq_lengths), config,
+        layer, softmax_scale, split_size, num_splits, batch_count,
+        stream_handle(stream))
+
+
+def flash_attention_append_decode_paged_bf16(out, partial_m, partial_l, partial_acc,
+                                             q, cache_k, cache_v, page_table,
+                                             seq_lengths, token_position, k, v,
+                                             config, layer, softmax_scale,
+                                             split_size, num_splits, batch_count,
+                                             stream=None) -> int:
+    return lib().gemma4_flash_attention_append_decode_paged_bf16(
+        ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(q),
+        ptr(cache_k), ptr(cache_v), ptr(page_table), ptr(seq_lengths),
+        ptr(token_position), ptr(k), ptr(v), config, layer, softmax_scale,
+        split_size, num_splits, batch_count, stream_handle(stream))

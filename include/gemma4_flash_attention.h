@@ -1,0 +1,76 @@
+// Decode and prefill attention over gemma.c's paged bf16 K/V cache,
+// MI355X (gfx950) build. All entry points are extern "C", stream-ordered,
+// allocate nothing, and return hipErrorInvalidValue on bad geometry or null
+// pointers before any launch (the reference convention,
+// src/gemma4_flash_attention_decode.cu:1121-1157).
+#pragma once
+
+#include "gemma4_kv_cache.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// Paged split-K decode attention (flash decoding) for one cache layer.
+//
+// The reference removed its standalone decode entry point and keeps the
+// attention as phases of a cooperative layer kernel; this signature is the
+// standalone form of those phases: phase_decode_paged_grouped_split
+// (src/gemma4_flash_attention_decode.cu:691-878) + phase_decode_paged_reduce
+// (src/gemma4_flash_attention_decode.cu:880-977), extended from batch 1 to
+// `batch_count` rows as their batch-indexed signatures allow.
+//
+//   d_out          [batch_count][16][head_dim] bf16
+//   d_q            [batch_count][16][head_dim] bf16 (prepared Q)
+//   d_seq_lengths  [batch_count] live length per sequence; the live keys are
+//                  [max(0, len - window_size), len) for a sliding cache and
+//                  [0, len) for a global one
+//   d_page_table   [batch_size][max_pages_per_seq] physical page per ring slot
+//   partials       partial_m/l [(row * num_splits + split)],
+//                  partial_acc [(row * num_splits + split) * head_dim + d],
+//                  row = b * 16 + q_head. Unused when num_splits == 1 (the
+//                  single split writes d_out directly; may then be null).
+// Split `s` covers live keys [first + s*split_size, first + (s+1)*split_size);
+// splits past the live count do nothing. Supported geometries:
+// (num_heads, head_dim) = (8, 256) and (1, 512); 16 query heads.
+hipError_t gemma4_flash_attention_decode_paged_bf16(
+    gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
+    float *d_partial_acc, const gemma4_bf16 *d_q, const gemma4_bf16 *d_cache_k,
+    const gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+    const int32_t *d_seq_lengths, Gemma4KvCacheConfig config, int32_t layer,
+    float softmax_scale, int32_t split_size, int32_t num_splits,
+    int32_t batch_count, hipStream_t stream);
+
+// Fused decode step: appends the current token's prepared K/V
+// (d_k/d_v [batch_count][num_heads][head_dim]) at d_token_position[b] with the
+// skip rules of gemma4_kv_cache_write_bf16 (token_batch[b] == b), then attends
+// exactly as gemma4_flash_attention_decode_paged_bf16. One launch (two with
+// the split combine); the split holding the new key reads it from d_k/d_v
+// while writing it, so the result equals append-then-attend bit for bit in
+// the cache and in the attention inputs. Replaces the append + attention
+// phases of decode_megakernel_fused_layer_kernel
+// (src/gemma4_flash_attention_decode.cu:306-375, 979-1034) without the
+// RMSNorm/RoPE preparation (K/V arrive prepared).
+hipError_t gemma4_flash_attention_append_decode_paged_bf16(
+    gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
+    float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+    const int32_t *d_seq_lengths, const int32_t *d_token_position,
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, Gemma4KvCacheConfig config,
+    int32_t layer, float softmax_scale, int32_t split_size, int32_t num_splits,
+    int32_t batch_count, hipStream_t stream);
+
+// Split plan for the MI355X: the split size (a multiple of the kernel's key
+// tile) that gives about `target_workgroups` split workgroups (0 = default,
+// two per CU) for `batch_count` sequences of up to `max_live_keys` live keys,
+// and the split count that covers `max_live_keys`. Replaces the fixed
+// GEMMA4_SLIDING_DECODE_SPLIT_SIZE (src/gemma4.h:24) and the active split
+// count of src/gemma4_decode_megakernel.cu:158-167.
+hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
+                                    int32_t batch_count, int32_t max_live_keys,
+                                    int32_t target_workgroups,
+                                    int32_t *split_size, int32_t *num_splits);
+
+#ifdef __cplusplus
+}  // extern "C"
+#endif

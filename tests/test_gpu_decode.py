@@ -1,0 +1,239 @@
+"""Parity of the HIP split-K decode attention (and its fused-append form)
+against the CPU oracle, within the north-star tolerance (max_abs 2e-2,
+max_rel 1e-2 with denominator max(|a|,|b|,1)), and at full BASELINE sizes
+against an fp32 torch reference plus size-independent properties."""
+import math
+
+import numpy as np
+import pytest
+
+import gemma_kv as gk
+from kvtest import (assert_close, cache_config, empty_bf16, fill_page_table,
+                    from_dev_bf16, randn_bf16, ring_pages, to_dev,
+                    torch_decode_reference)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_decode(dev, cfg, q, ck, cv, pt, seq, layer, scale, split_size, num_splits,
+                fused=None):
+    import torch
+    batch = len(seq)
+    dim = cfg[6]
+    out = empty_bf16((batch, 16, dim), dev)
+    rows = batch * 16 * num_splits
+    pm = torch.full((rows,), float("nan"), device=dev)
+    pl = torch.full((rows,), float("nan"), device=dev)
+    pa = torch.full((rows * dim,), float("nan"), device=dev)
+    args = dict(config=gk.make_config(*cfg), layer=layer, softmax_scale=scale,
+                split_size=split_size, num_splits=num_splits, batch_count=batch)
+    if fused is None:
+        code = gk.flash_attention_decode_paged_bf16(
+            out, pm, pl, pa, to_dev(q, dev), ck, cv, to_dev(pt, dev),
+            to_dev(np.asarray(seq, np.int32), dev), **args)
+    else:
+        pos, k_new, v_new = fused
+        code = gk.flash_attention_append_decode_paged_bf16(
+            out, pm, pl, pa, to_dev(q, dev), ck, cv, to_dev(pt, dev),
+            to_dev(np.asarray(seq, np.int32), dev), to_dev(np.asarray(pos, np.int32), dev),
+            to_dev(k_new, dev), to_dev(v_new, dev), **args)
+    gk.check(code, "decode")
+    torch.cuda.synchronize()
+    return from_dev_bf16(out)
+
+
+CASES = [
+    # heads, dim, page, window, seq_lengths, split_size, num_splits
+    (8, 256, 1, 1024, [1], 32, 1),
+    (8, 256, 1, 1024, [33], 32, 2),
+    (8, 256, 1, 1024, [1024], 32, 32),
+    (8, 256, 1, 1024, [3000], 128, 8),          # ring wrapped
+    (8, 256, 1, 1024, [1500], 1024, 1),         # single split, direct output
+    (8, 256, 64, 1024, [2500, 77], 96, 11),     # page-64 ring, batch 2
+    (8, 256, 64, 0, [4096, 1, 700], 256, 16),   # global, ragged batch
+    (8, 256, 16, 0, [0, 513], 64, 9),           # empty sequence in a batch
+    (8, 256, 1, 1024, [0], 32, 1),              # empty, direct zeros
+    (8, 256, 64, 0, [2000], 20, 100),           # the reference split size 20
+    (1, 512, 64, 0, [300, 4100], 128, 33),      # reference global geometry
+    (1, 512, 64, 0, [65], 512, 1),
+]
+
+
+@pytest.mark.parametrize("heads,dim,page,window,seq,split_size,num_splits", CASES)
+def test_decode_matches_oracle(dev, heads, dim, page, window, seq, split_size, num_splits):
+    rng = np.random.default_rng(sum(seq) + split_size)
+    batch = len(seq)
+    max_pages = ring_pages(window, page) if window else (max(max(seq), 1) + page - 1) // page
+    cfg = cache_config(2, batch, page, max_pages, heads, dim, window)
+    pt = fill_page_table(cfg, seq)
+    n_rows = 2 * batch * max_pages * page
+    ck = randn_bf16(rng, (n_rows, heads, dim))
+    cv = randn_bf16(rng, (n_rows, heads, dim))
+    q = randn_bf16(rng, (batch, 16, dim))
+    scale = 1.0 / math.sqrt(dim)
+    exp = oracle.decode_attention(q, ck, cv, pt, seq, cfg, 1, scale)
+    got = _run_decode(dev, cfg, q, to_dev(ck, dev), to_dev(cv, dev), pt, seq, 1, scale,
+                      split_size, num_splits)
+    assert_close(got, exp, f"seq={seq}")
+    for b, n in enumerate(seq):
+        if n == 0:
+            assert not got[b].any()
+
+
+def test_decode_skips_unmapped_pages(dev):
+    rng = np.random.default_rng(11)
+    heads, dim, page = 8, 256, 16
+    seq = [900]
+    cfg = cache_config(1, 1, page, 64, heads, dim, 0)
+    pt = fill_page_table(cfg, seq)
+    pt[[3, 17, 18]] = -1
+    pt[40] = 10_000  # out-of-range physical page
+    ck = randn_bf16(rng, (64 * page, heads, dim))
+    cv = randn_bf16(rng, (64 * page, heads, dim))
+    q = randn_bf16(rng, (1, 16, dim))
+    exp = oracle.decode_attention(q, ck, cv, pt, seq, cfg, 0, 0.0625)
+    got = _run_decode(dev, cfg, q, to_dev(ck, dev), to_dev(cv, dev), pt, seq, 0, 0.0625, 64, 15)
+    assert_close(got, exp, "unmapped pages")
+
+
+def test_decode_outlier_keys_max_tracking(dev):
+    # 1% of keys scaled x8 (BASELINE long-context stress), many small splits.
+    rng = np.random.default_rng(5)
+    heads, dim, page = 8, 256, 64
+    seq = [8192]
+    cfg = cache_config(1, 1, page, 128, heads, dim, 0)
+    pt = fill_page_table(cfg, seq)
+    kf = rng.standard_normal((8192, heads, dim), dtype=np.float32)
+    hot = rng.choice(8192, size=82, replace=False)
+    kf[hot] *= 8.0
+    ck = oracle.f32_to_bf16(kf)
+    cv = randn_bf16(rng, (8192, heads, dim))
+    q = randn_bf16(rng, (1, 16, dim))
+    exp = oracle.decode_attention(q, ck, cv, pt, seq, cfg, 0, 1 / 16)
+    got = _run_decode(dev, cfg, q, to_dev(ck, dev), to_dev(cv, dev), pt, seq, 0, 1 / 16, 128, 64)
+    assert_close(got, exp, "outliers")
+
+
+@pytest.mark.parametrize("heads,dim,page,window,seq_before,split_size,num_splits", [
+    (8, 256, 1, 1024, 2047, 64, 16),   # ring slot reuse, new token in the last split
+    (8, 256, 64, 1024, 130, 32, 5),
+    (8, 256, 64, 0, 5000, 512, 10),
+    (1, 512, 64, 0, 777, 64, 13),
+    (8, 256, 1, 1024, 0, 32, 1),       # first token of a sequence
+])
+def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, window,
+                                                       seq_before, split_size, num_splits):
+    rng = np.random.default_rng(seq_before + 3)
+    batch = 2
+    seq = [seq_before + 1, max(1, seq_before // 3 + 1)]
+    max_pages = ring_pages(window, page) if window else (max(seq) + page - 1) // page
+    cfg = cache_config(1, batch, page, max_pages, heads, dim, window)
+    pt = fill_page_table(cfg, seq)
+    n_rows = batch * max_pages * page
+    ck0 = randn_bf16(rng, (n_rows, heads, dim))
+    cv0 = randn_bf16(rng, (n_rows, heads, dim))
+    q = randn_bf16(rng, (batch, 16, dim))
+    k_new = randn_bf16(rng, (batch, heads, dim))
+    v_new = randn_bf16(rng, (batch, heads, dim))
+    pos = [n - 1 for n in seq]
+    exp_k, exp_v = ck0.copy(), cv0.copy()
+    oracle.kv_cache_write(exp_k, exp_v, cfg, pt, list(range(batch)), pos, 0, k_new, v_new)
+    exp = oracle.decode_attention(q, exp_k, exp_v, pt, seq, cfg, 0, 1 / math.sqrt(dim))
+    ck, cv = to_dev(ck0, dev), to_dev(cv0, dev)
+    got = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, 1 / math.sqrt(dim), split_size,
+                      num_splits, fused=(pos, k_new, v_new))
+    assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
+    assert np.array_equal(from_dev_bf16(cv).reshape(exp_v.shape), exp_v)
+    assert_close(got, exp, "fused")
+    # The unfused kernel on the appended cache gives the same bits.
+    unfused = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, 1 / math.sqrt(dim), split_size,
+                          num_splits)
+    assert np.array_equal(unfused, got)
+
+
+def test_split_count_invariance_closed_forms(dev):
+    import torch
+    rng = np.random.default_rng(99)
+    heads, dim, page = 8, 256, 64
+    seq = [3333]
+    cfg = cache_config(1, 1, page, 64, heads, dim, 0)
+    pt = fill_page_table(cfg, seq)
+    ck = randn_bf16(rng, (64 * page, heads, dim))
+    cv = randn_bf16(rng, (64 * page, heads, dim))
+    q = randn_bf16(rng, (1, 16, dim))
+    dck, dcv = to_dev(ck, dev), to_dev(cv, dev)
+    outs = [oracle.bf16_to_f32(_run_decode(dev, cfg, q, dck, dcv, pt, seq, 0, 1 / 16, s, n))
+            for s, n in [(3333, 1), (32, 105), (224, 15), (1024, 4)]]
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() <= 2 ** -7  # bf16 rounding of fp32-equal values
+    # q = 0 -> uniform weights -> mean of the live V rows.
+    zq = np.zeros_like(q)
+    got = oracle.bf16_to_f32(_run_decode(dev, cfg, zq, dck, dcv, pt, seq, 0, 1 / 16, 256, 14))
+    mean = oracle.bf16_to_f32(cv[:3333]).astype(np.float64).mean(axis=0)  # [heads, dim]
+    expect = np.repeat(mean, 2, axis=0)
+    assert np.abs(got[0] - expect).max() <= 2e-3
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("case", ["config2_global_8192", "config4_131072_outliers",
+                                  "config3_batch64_mixed"])
+def test_full_size_against_torch_fp32(dev, case):
+    """BASELINE sizes: HIP vs an fp32 torch reference of the same paged gather."""
+    import torch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(2024)
+    heads, dim, page = 8, 256, 64
+    if case == "config2_global_8192":
+        seq = [8192]
+    elif case == "config4_131072_outliers":
+        seq = [131072]
+    else:
+        rng = np.random.default_rng(64)
+        seq = rng.integers(512, 32769, size=64).tolist()
+    batch = len(seq)
+    max_pages = (max(seq) + page - 1) // page
+    cfg = cache_config(1, batch, page, max_pages, heads, dim, 0)
+    pt = fill_page_table(cfg, seq)
+    n_rows = batch * max_pages * page
+    ck = torch.randn((n_rows, heads, dim), generator=gen, device=dev).bfloat16()
+    if case == "config4_131072_outliers":
+        hot = torch.randperm(n_rows, generator=gen, device=dev)[: n_rows // 100]
+        ck[hot] *= 8
+    cv = torch.randn((n_rows, heads, dim), generator=gen, device=dev).bfloat16()
+    q = torch.randn((batch, 16, dim), generator=gen, device=dev).bfloat16()
+    split_size, num_splits = gk.decode_split_plan(gk.make_config(*cfg), batch, max(seq))
+    out = empty_bf16((batch, 16, dim), dev)
+    rows = batch * 16 * num_splits
+    pm = torch.empty(rows, device=dev)
+    pl = torch.empty(rows, device=dev)
+    pa = torch.empty(rows * dim, device=dev)
+    ck_i, cv_i, q_i = ck.view(torch.int16), cv.view(torch.int16), q.view(torch.int16)
+    gk.check(gk.flash_attention_decode_paged_bf16(
+        out, pm, pl, pa, q_i, ck_i, cv_i, to_dev(pt, dev), to_dev(np.asarray(seq, np.int32), dev),
+        gk.make_config(*cfg), 0, 1 / 16, split_size, num_splits, batch))
+    ref = torch_decode_reference(q_i, ck_i, cv_i, pt, seq, cfg, 0, 1 / 16)
+    got = out.view(torch.bfloat16).float()
+    ref_b = ref.bfloat16().float()
+    diff = (got - ref_b).abs()
+    rel = diff / torch.maximum(torch.maximum(got.abs(), ref_b.abs()), torch.ones_like(got))
+    assert diff.max().item() <= 2e-2 and rel.max().item() <= 1e-2, (diff.max().item(), rel.max().item())
+    assert torch.isfinite(got).all()
+
+
+def test_decode_error_convention(dev):
+    cfg = gk.make_config(40, 1024, 1, 1024, 1, 8, 256, 1024)
+    buf = empty_bf16(1 << 16, dev)
+    idx = to_dev(np.zeros(1024, np.int32), dev)
+    f = gk.flash_attention_decode_paged_bf16
+    inval = gk.HIP_ERROR_INVALID_VALUE
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, cfg, 0, 0.0625, 32, 1, 0) == 0
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, cfg, 40, 0.0625, 32, 1, 1) == inval
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, cfg, 0, 0.0, 32, 1, 1) == inval
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, cfg, 0, 0.0625, 0, 1, 1) == inval
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, cfg, 0, 0.0625, 32, 4, 1) == inval  # no partials
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, cfg, 0, 0.0625, 32, 1, 2) == inval  # batch > batch_size
+    small_ring = gk.make_config(40, 512, 1, 512, 1, 8, 256, 1024)  # capacity < window
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, small_ring, 0, 0.0625, 32, 1, 1) == inval
+    odd = gk.make_config(40, 1024, 1, 1024, 1, 4, 128, 1024)  # unsupported geometry
+    assert f(buf, None, None, None, buf, buf, buf, idx, idx, odd, 0, 0.0625, 32, 1, 1) == inval
