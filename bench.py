@@ -1,0 +1,379 @@
+"""Benchmark: decode attention + KV append, µs per layer-step and achieved HBM
+GB/s on one MI355X.
+
+Workload: one full-depth batch-1 decode step = 48 layers in
+gemma4 order (40 sliding layers with 1024-slot rings, page 1; 8 global layers,
+page 64), 8 KV heads x 256, 16 query heads, bf16, context 8192 prefilled with
+N(0,1) K/V. Each layer appends the current token (position 8192) and attends
+over its live keys with one fused HIP launch (append + split-K attention +
+in-kernel split combine). Every timed step does the full work; the appended
+position is the same each step so the per-step work is constant.
+
+`value` = algorithmic HBM bytes of a step / step time (graph-replayed), with
+all inputs resident in HBM. Also reported: the eager per-launch rate, the
+batch-64 global-layer rate, the roofline of the dominant
+kernel measured live with HIP events, and the CPU oracle baseline.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "gemma.c_amd"))
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBS = 8000.0
+NUM_LAYERS = 48
+HEADS, DIM, QH = 8, 256, 16
+CONTEXT = 8192
+WINDOW = 1024
+GLOBAL_PAGE = 64
+ROW_BYTES = HEADS * DIM * 2  # one token's K (or V) row, all KV heads
+
+
+def is_global_layer(layer: int) -> bool:
+    """gemma4 5:1 cadence with the last layer global (src/gemma4.h:105-108)."""
+    return layer == NUM_LAYERS - 1 or (layer + 1) % 6 == 0
+
+
+def layer_bytes(live_keys: int, batch: int = 1) -> int:
+    """Algorithmic HBM bytes of one fused layer step: K+V of every live key
+    (the new key included), the appended K/V row write, and q/out rows."""
+    kv_read = live_keys * 2 * ROW_BYTES
+    append = batch * 2 * ROW_BYTES
+    q_out = batch * 2 * QH * DIM * 2
+    return kv_read + append + q_out
+
+
+class Layer:
+    pass
+
+
+def build_config2(torch, gk, dev, seed=0):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    seq_len = CONTEXT + 1
+    sliding_pages = WINDOW  # page size 1 -> exactly 1024 ring slots
+    global_pages = (seq_len + GLOBAL_PAGE - 1) // GLOBAL_PAGE
+    n_sliding = sum(1 for l in range(NUM_LAYERS) if not is_global_layer(l))
+    n_global = NUM_LAYERS - n_sliding
+    s_cfg = gk.make_config(n_sliding, sliding_pages, 1, sliding_pages, 1, HEADS, DIM, WINDOW)
+    g_cfg = gk.make_config(n_global, global_pages, GLOBAL_PAGE, global_pages, 1, HEADS, DIM, 0)
+
+    def randn_bf16(shape):
+        return torch.randn(shape, generator=gen, device=dev, dtype=torch.float32).bfloat16().view(torch.int16)
+
+    caches = {
+        "sk": randn_bf16((n_sliding * sliding_pages, HEADS, DIM)),
+        "sv": randn_bf16((n_sliding * sliding_pages, HEADS, DIM)),
+        "gk": randn_bf16((n_global * global_pages * GLOBAL_PAGE, HEADS, DIM)),
+        "gv": randn_bf16((n_global * global_pages * GLOBAL_PAGE, HEADS, DIM)),
+    }
+    i32 = dict(dtype=torch.int32, device=dev)
+    meta = {
+        "s_pt": torch.arange(sliding_pages, **i32),
+        "g_pt": torch.arange(global_pages, **i32),
+        "seq": torch.tensor([seq_len], **i32),
+        "pos": torch.tensor([CONTEXT], **i32),
+    }
+    s_split, s_n = gk.decode_split_plan(s_cfg, 1, WINDOW)
+    g_split, g_n = gk.decode_split_plan(g_cfg, 1, seq_len)
+    max_n = max(s_n, g_n)
+    scratch = {
+        "pm": torch.empty(QH * max_n, device=dev),
+        "pl": torch.empty(QH * max_n, device=dev),
+        "pa": torch.empty(QH * max_n * DIM, device=dev),
+        "cnt": torch.zeros(HEADS, **i32),
+    }
+    layers = []
+    si = gi = 0
+    for l in range(NUM_LAYERS):
+        L = Layer()
+        L.is_global = is_global_layer(l)
+        if L.is_global:
+            L.cfg, L.cache_layer, L.ck, L.cv, L.pt = g_cfg, gi, caches["gk"], caches["gv"], meta["g_pt"]
+            L.split, L.n_splits, L.live = g_split, g_n, seq_len
+            gi += 1
+        else:
+            L.cfg, L.cache_layer, L.ck, L.cv, L.pt = s_cfg, si, caches["sk"], caches["sv"], meta["s_pt"]
+            L.split, L.n_splits, L.live = s_split, s_n, WINDOW
+            si += 1
+        L.q = randn_bf16((1, QH, DIM))
+        L.k = randn_bf16((1, HEADS, DIM))
+        L.v = randn_bf16((1, HEADS, DIM))
+        L.out = torch.zeros((1, QH, DIM), dtype=torch.int16, device=dev)
+        L.bytes = layer_bytes(L.live)
+        layers.append(L)
+    return layers, caches, meta, scratch
+
+
+def launch_layer(gk, L, meta, scratch, stream):
+    return gk.flash_attention_append_decode_paged_bf16(
+        L.out, scratch["pm"], scratch["pl"], scratch["pa"], L.q, L.ck, L.cv, L.pt,
+        meta["seq"], meta["pos"], L.k, L.v, L.cfg, L.cache_layer, 1.0 / math.sqrt(DIM),
+        L.split, L.n_splits, 1, stream=stream, split_counters=None)
+
+
+def time_graph(torch, fn, reps, warmup):
+    """Capture fn() once as a HIP graph; replay `reps` times between events."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(s.cuda_stream)  # warm the code objects outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn(torch.cuda.current_stream().cuda_stream)
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps, g
+
+
+def time_eager(torch, fn, reps, warmup):
+    st = torch.cuda.current_stream().cuda_stream
+    for _ in range(warmup):
+        fn(st)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn(st)
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def read_traffic(kernel_tag: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = REPO / "profiles" / f"{kernel_tag}_pmc.md"
+    if not path.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    return float(m.group(1)) if m else None
+
+
+def bench_batch64(torch, gk, dev, steps, warmup):
+    """one global layer, 64 sequences, contexts U[512, 32768]."""
+    import numpy as np
+    rng = np.random.default_rng(64)
+    seq = rng.integers(512, 32769, size=64).astype(np.int32)
+    page = GLOBAL_PAGE
+    max_pages = (int(seq.max()) + page - 1) // page
+    cfg = gk.make_config(1, 64 * max_pages, page, max_pages, 64, HEADS, DIM, 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+    rows = 64 * max_pages * page
+    ck = torch.empty((rows, HEADS, DIM), dtype=torch.bfloat16, device=dev)
+    cv = torch.empty_like(ck)
+    for t in (ck, cv):  # fill in slices to bound the fp32 temporary
+        for r0 in range(0, rows, 1 << 20):
+            t[r0:r0 + (1 << 20)] = torch.randn((min(1 << 20, rows - r0), HEADS, DIM),
+                                               generator=gen, device=dev).bfloat16()
+    ck, cv = ck.view(torch.int16), cv.view(torch.int16)
+    pt = torch.arange(64 * max_pages, dtype=torch.int32, device=dev)
+    seq_t = torch.from_numpy(seq).to(dev)
+    pos_t = torch.from_numpy(seq - 1).to(dev)
+    q = torch.randn((64, QH, DIM), generator=gen, device=dev).bfloat16().view(torch.int16)
+    k = torch.randn((64, HEADS, DIM), generator=gen, device=dev).bfloat16().view(torch.int16)
+    v = torch.randn((64, HEADS, DIM), generator=gen, device=dev).bfloat16().view(torch.int16)
+    out = torch.zeros((64, QH, DIM), dtype=torch.int16, device=dev)
+    split, n = gk.decode_split_plan(cfg, 64, int(seq.max()))
+    pm = torch.empty(64 * QH * n, device=dev)
+    pl = torch.empty_like(pm)
+    pa = torch.empty(64 * QH * n * DIM, device=dev)
+    cnt = torch.zeros(64 * HEADS, dtype=torch.int32, device=dev)
+
+    def fn(st):
+        gk.check(gk.flash_attention_append_decode_paged_bf16(
+            out, pm, pl, pa, q, ck, cv, pt, seq_t, pos_t, k, v, cfg, 0, 1 / 16, split, n, 64,
+            stream=st, split_counters=cnt), "batch64 decode")
+
+    ms, _ = time_graph(torch, fn, steps, warmup)
+    total = sum(layer_bytes(int(s)) for s in seq)
+    gbs = total / (ms * 1e-3) / 1e9
+    del ck, cv
+    return {"workload": "config3: 1 global layer, 64 seqs, ctx U[512,32768] seed 64",
+            "us_per_layer_step": ms * 1e3, "achieved_GBs": gbs,
+            "frac_of_peak": gbs / HBM_PEAK_GBS, "split_size": split, "num_splits": n,
+            "bytes_per_step": total}
+
+
+def cpu_baseline(max_seconds: float):
+    """BASELINE config 1 on the host with the C oracle (1 thread): single
+    sliding layer, 8x256 KV, 16 q heads, 1024-slot ring (page 1), sequential
+    append+attend steps from an empty cache; bounded to about `max_seconds`."""
+    import numpy as np
+    from oracle import oracle
+    rng = np.random.default_rng(1)
+    cfg = (1, WINDOW, 1, WINDOW, 1, HEADS, DIM, WINDOW)
+    ck = np.zeros(WINDOW * HEADS * DIM, np.uint16)
+    cv = np.zeros_like(ck)
+    pt = np.full(WINDOW, -1, np.int32)
+    slots = np.full(WINDOW, -1, np.int32)
+    scale = 1.0 / 16.0
+    total_bytes = 0
+    steps = 0
+    t0 = time.perf_counter()
+    elapsed = 0.0
+    compute = 0.0
+    for step in range(2048):
+        q = oracle.f32_to_bf16(rng.standard_normal((1, QH, DIM), dtype=np.float32))
+        k = oracle.f32_to_bf16(rng.standard_normal((1, HEADS, DIM), dtype=np.float32))
+        v = oracle.f32_to_bf16(rng.standard_normal((1, HEADS, DIM), dtype=np.float32))
+        assert oracle.ensure_page(pt, slots, cfg, 0, step) >= 0
+        c0 = time.perf_counter()
+        oracle.kv_cache_write(ck, cv, cfg, pt, [0], [step], 0, k, v)
+        oracle.decode_attention(q, ck, cv, pt, [step + 1], cfg, 0, scale)
+        compute += time.perf_counter() - c0
+        total_bytes += layer_bytes(min(step + 1, WINDOW))
+        steps += 1
+        elapsed = time.perf_counter() - t0
+        if elapsed > max_seconds:
+            break
+    return {"value": total_bytes / compute / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "us_per_layer_step": compute / steps * 1e6, "steps": steps,
+            "sample": f"config1 steps 0..{steps - 1} of 2048 (ring 1024, 8x256 KV, 16 q heads), "
+                      f"C oracle -O3 single thread, append+attend per step, {compute:.1f} s",
+            "cpu_model": _cpu_model(), "host_threads": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-batch64", action="store_true")
+    ap.add_argument("--only", choices=["step", "global", "copy"], default=None,
+                    help="profiling helper: run one leg only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: the KV-cache path runs on a single MI355X and "
+              f"has no multi-GPU leg (asked for --gpus {args.gpus}).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import gemma_kv as gk
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    gk.lib()
+    dev = torch.device("cuda:0")
+
+    if args.only == "copy":
+        # Calibration kernel for the PMC byte counters: a 1 GiB device copy.
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}))
+        return
+
+    layers, caches, meta, scratch = build_config2(torch, gk, dev)
+    step_bytes = sum(L.bytes for L in layers)
+
+    def step(stream):
+        for L in layers:
+            code = launch_layer(gk, L, meta, scratch, stream)
+            if code:
+                raise gk.HipError(code, "append_decode")
+
+    if args.only == "step":
+        for _ in range(args.steps):
+            step(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return
+
+    # ---- dominant kernel: the global-layer launch, live HIP-event timing
+    g_layers = [L for L in layers if L.is_global]
+
+    def global_round(stream):
+        for L in g_layers:
+            gk.check(launch_layer(gk, L, meta, scratch, stream), "global layer")
+
+    if args.only == "global":
+        for _ in range(args.steps):
+            global_round(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        return
+
+    g_rounds = 20
+    g_ms, _ = time_graph(torch, lambda st: [global_round(st) for _ in range(g_rounds)], 3, 1)
+    g_launch_us = g_ms * 1e3 / (g_rounds * len(g_layers))
+    g_bytes = g_layers[0].bytes
+    g_gbs = g_bytes / (g_launch_us * 1e-6) / 1e9
+    traffic = read_traffic("decode_split_global_ctx8192")
+
+    # ---- the headline: full 48-layer step, graph replay and eager
+    torch.cuda.synchronize()
+    ms_graph, _ = time_graph(torch, step, args.steps, args.warmup)
+    ms_eager = time_eager(torch, step, max(5, args.steps // 5), 2)
+    gbs = step_bytes / (ms_graph * 1e-3) / 1e9
+    gbs_eager = step_bytes / (ms_eager * 1e-3) / 1e9
+
+    result = {
+        "metric": "decode attn+KV-append µs/layer-step and achieved HBM GB/s at batch 1 and 64",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_graph, 4),
+        "us_per_layer_step": round(ms_graph * 1e3 / NUM_LAYERS, 3),
+        "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/q from a fixed seed",
+        "config": {"workload": "config2: 48 layers (40 sliding ring-1024 page-1 + 8 global page-64), "
+                               "8 KV heads x 256, 16 q heads, batch 1, context 8192, fused append+decode",
+                   "batch": 1, "context": CONTEXT, "layers": NUM_LAYERS,
+                   "bytes_per_step": step_bytes, "timing": "hipGraph replay of the 48 launches"},
+        "eager": {"ms_per_step": round(ms_eager, 4),
+                  "us_per_layer_step": round(ms_eager * 1e3 / NUM_LAYERS, 3),
+                  "achieved_GBs": round(gbs_eager, 1)},
+        "roofline": {"kernel": "decode_split_kernel<8x256> global layer (ctx 8193, fused append+combine)",
+                     "bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(g_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": traffic, "avg_launch_us": round(g_launch_us, 3),
+                     "algorithmic_bytes_per_launch": g_bytes},
+    }
+    if not args.no_batch64:
+        b64 = bench_batch64(torch, gk, dev, max(3, args.steps // 5), 2)
+        result["batch64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in b64.items()}
+    del caches
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -4,7 +4,7 @@
 // phase_decode_paged_reduce, phase_decode_q_paged_kv_norm_rope's cache write).
 //
 // Work decomposition
-//   workgroup (split, kv_head, batch)   grid = (num_splits, num_heads, batch)
+//   workgroup (kv_head, split, batch)   grid = (num_heads, num_splits, batch)
 //   wave                                a key tile of kTileKeys keys at a time
 //   lane (r, c)                         c = dim pack (8 bf16 = 16 bytes) of
 //                                       key row r of each 128-bit load
@@ -47,6 +47,7 @@ struct DecodeParams {
   const int32_t *page_table;
   const int32_t *seq_lengths;
   const int32_t *token_position;  // null: no append
+  int32_t *counters;              // null: separate combine kernel
   const uint16_t *new_k;
   const uint16_t *new_v;
   Gemma4KvCacheConfig c;
@@ -56,7 +57,7 @@ struct DecodeParams {
   int32_t num_splits;
 };
 
-template <int kHeads, int kDim, int kHeadsPerWave, int kLoads>
+template <int kHeads, int kDim, int kHeadsPerWave, int kLoads, int kChunkTiles>
 struct DecodeShape {
   static constexpr int G = kQueryHeads / kHeads;          // GQA group
   static constexpr int GW = kHeadsPerWave;                // heads per wave
@@ -65,6 +66,7 @@ struct DecodeShape {
   static constexpr int RPL = kWave / LPR;                 // rows per load
   static constexpr int LOADS = kLoads;                    // loads per lane per tile
   static constexpr int KT = RPL * kLoads;                 // keys per tile
+  static constexpr int CT = kChunkTiles;                  // tiles per page-lookup chunk
   static constexpr int NP = kLoads * GW;                  // partial dots per lane
   static constexpr int S = __builtin_ctz(LPR / NP);       // duplicate-lane bits
   static constexpr int GB = __builtin_ctz(GW);            // head-select bits
@@ -72,14 +74,16 @@ struct DecodeShape {
   static_assert(G % GW == 0, "heads per wave must divide the GQA group");
   static_assert(NP <= LPR, "one reduced score per lane at most");
   static_assert((NP & (NP - 1)) == 0 && (GW & (GW - 1)) == 0, "powers of two");
-  static_assert(KT <= kWave, "one page lookup per lane per tile");
+  static_assert(KT * kChunkTiles <= kWave, "one page lookup per lane per chunk");
   static_assert(RPL * NP <= kWave, "probability slot holds one tile");
 };
 
 // Value-splitting butterfly: N partial values per lane are summed over the
-// lanes that differ in bits [log2(O*2/N).. log2(O)] of the lane id; after the
-// split steps every lane carries one value, and remaining offsets are plain
-// all-reduce steps (the value then repeats across those lanes).
+// 2*O lanes of a group (bit O first, down to bit 1); each exchange sends the
+// half of the values the partner keeps, so after log2(N) steps every lane
+// carries one fully reduced value, whose index is given by the lane bits
+// [log2(O*2/N), log2(O)]. Remaining offsets are plain all-reduce steps (the
+// value then repeats across those low lanes).
 template <int N, int O>
 __device__ __forceinline__ void split_butterfly(float *v, int lane) {
   if constexpr (N > 1) {
@@ -88,38 +92,50 @@ __device__ __forceinline__ void split_butterfly(float *v, int lane) {
     for (int i = 0; i < N / 2; ++i) {
       const float send = hi ? v[i] : v[i + N / 2];
       const float keep = hi ? v[i + N / 2] : v[i];
-      v[i] = keep + xor_lane(send, O);
+      v[i] = keep + lane_pair<O>(send);
     }
     split_butterfly<N / 2, O / 2>(v, lane);
   } else if constexpr (O >= 1) {
-    v[0] += xor_lane(v[0], O);
+    v[0] += lane_pair<O>(v[0]);
     split_butterfly<1, O / 2>(v, lane);
   }
 }
 
-// Max / sum of one value over all lanes whose bit pattern differs only at
-// offsets >= kFrom (lanes below kFrom carry duplicates or another head).
+// Max / sum of one value over all lanes that differ only in lane bits at or
+// above kFrom (lower bits select duplicates or another GQA head).
 template <int kFrom>
 __device__ __forceinline__ float reduce_max_from(float v) {
-#pragma unroll
-  for (int o = kFrom; o < kWave; o <<= 1) v = fmaxf(v, xor_lane(v, o));
-  return v;
+  if constexpr (kFrom < kWave) {
+    v = fmaxf(v, lane_xor<kFrom>(v));
+    return reduce_max_from<kFrom * 2>(v);
+  } else {
+    return v;
+  }
 }
 template <int kFrom>
 __device__ __forceinline__ float reduce_sum_from(float v) {
-#pragma unroll
-  for (int o = kFrom; o < kWave; o <<= 1) v += xor_lane(v, o);
-  return v;
+  if constexpr (kFrom < kWave) {
+    v += lane_xor<kFrom>(v);
+    return reduce_sum_from<kFrom * 2>(v);
+  } else {
+    return v;
+  }
 }
 
 // Collect a per-head value held by the lanes of head `my_g` into out[g] for
 // every head g of the wave (lanes of head g differ in bits [S, S+GB)).
+template <int GW, int S, int D = 1>
+__device__ __forceinline__ void gather_other(float mine, float (&other)[GW]) {
+  if constexpr (D < GW) {
+    other[D] = lane_xor<(D << S)>(mine);
+    gather_other<GW, S, D + 1>(mine, other);
+  }
+}
 template <int GW, int S>
 __device__ __forceinline__ void gather_heads(float mine, int my_g, float (&out)[GW]) {
   float other[GW];
   other[0] = mine;
-#pragma unroll
-  for (int d = 1; d < GW; ++d) other[d] = xor_lane(mine, d << S);
+  gather_other<GW, S>(mine, other);
 #pragma unroll
   for (int g = 0; g < GW; ++g) {
     const int d = my_g ^ g;
@@ -127,6 +143,17 @@ __device__ __forceinline__ void gather_heads(float mine, int my_g, float (&out)[
 #pragma unroll
     for (int dd = 1; dd < GW; ++dd) v = (d == dd) ? other[dd] : v;
     out[g] = v;
+  }
+}
+
+// Sum over the RPL key rows of a load (lane bits >= LPR).
+template <int LPR>
+__device__ __forceinline__ float sum_rows(float v) {
+  if constexpr (LPR < kWave) {
+    v += lane_xor<LPR>(v);
+    return sum_rows<LPR * 2>(v);
+  } else {
+    return v;
   }
 }
 
@@ -162,28 +189,130 @@ __device__ __forceinline__ int32_t append_row(const Gemma4KvCacheConfig &c,
   return key_row(c, page_table, layer, b, position);
 }
 
+// Device-coherent (sc1) accesses for data exchanged between workgroups of
+// one launch: they bypass the per-XCD L2 write-back state, so no whole-cache
+// maintenance is needed (agent-scope relaxed atomics compile to the same).
+constexpr int kCoherentAux = 16;  // cache-policy bit sc1
+__device__ __forceinline__ void coherent_store(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+using u32x4 = __attribute__((ext_vector_type(4))) unsigned;
+__device__ __forceinline__ void coherent_store8(float *p, const float (&v)[8]) {
+  const auto rsrc = __builtin_amdgcn_make_buffer_rsrc(p, 0, 32, 0x00020000);
+  const u32x4 lo = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]),
+                    __float_as_uint(v[3])};
+  const u32x4 hi = {__float_as_uint(v[4]), __float_as_uint(v[5]), __float_as_uint(v[6]),
+                    __float_as_uint(v[7])};
+  __builtin_amdgcn_raw_buffer_store_b128(lo, rsrc, 0, 0, kCoherentAux);
+  __builtin_amdgcn_raw_buffer_store_b128(hi, rsrc, 16, 0, kCoherentAux);
+}
+// Wait until this thread's outstanding memory operations have completed
+// (the signal fences keep the compiler from moving memory accesses across).
+__device__ __forceinline__ void wait_stores_complete() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Buffer view of `count` floats for coherent loads; out-of-range loads read 0.
+__device__ __forceinline__ auto coherent_view(const float *p, int32_t count) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), 0, count * 4, 0x00020000);
+}
+
+// Log-sum-exp combine of `splits` partials for GW consecutive query heads
+// starting at q_head0 of batch b, by one wave of the last-arriving split
+// workgroup, reading the other workgroups' partials with coherent loads that
+// are issued in independent batches (one memory round trip per batch).
+// Lane (r, cpack) owns dims [8*cpack, 8*cpack+8) and takes the splits
+// s == r (mod RPL); the RPL row groups are summed at the end. Same
+// arithmetic as decode_combine_kernel.
+template <int GW, int D, int LPR, int RPL>
+__device__ __forceinline__ void combine_row_group(const DecodeParams &p, int32_t b,
+                                                  int32_t q_head0, int32_t splits,
+                                                  int r, int cpack) {
+  constexpr int kBatch = 8;
+  const int lane = __lane_id();
+#pragma unroll 1
+  for (int g = 0; g < GW; ++g) {
+    const int64_t row = (int64_t)b * kQueryHeads + q_head0 + g;
+    const auto pm = coherent_view(p.partial_m + row * p.num_splits, splits);
+    const auto pl = coherent_view(p.partial_l + row * p.num_splits, splits);
+    const auto pa = coherent_view(p.partial_acc + row * p.num_splits * D, splits * D);
+    float big_m = -INFINITY;
+    for (int32_t s0 = 0; s0 < splits; s0 += kWave * 4) {
+      float mv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int32_t s = s0 + i * kWave + lane;
+        mv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pm, s * 4, 0, kCoherentAux));
+        mv[i] = s < splits ? mv[i] : -INFINITY;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) big_m = fmaxf(big_m, mv[i]);
+    }
+    big_m = reduce_max_from<1>(big_m);
+    float big_l = 0.0f;
+    float sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int32_t s0 = r; s0 < splits; s0 += kBatch * RPL) {
+      float ms[kBatch], ls[kBatch];
+      u32x4 lo[kBatch], hi[kBatch];
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const int32_t s = s0 + i * RPL;  // past `splits`: reads 0, weight 0
+        ms[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pm, s * 4, 0, kCoherentAux));
+        ls[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pl, s * 4, 0, kCoherentAux));
+        const int32_t off = (s * D + cpack * 8) * 4;
+        lo[i] = __builtin_amdgcn_raw_buffer_load_b128(pa, off, 0, kCoherentAux);
+        hi[i] = __builtin_amdgcn_raw_buffer_load_b128(pa, off + 16, 0, kCoherentAux);
+      }
+#pragma unroll
+      for (int i = 0; i < kBatch; ++i) {
+        const float w = ls[i] > 0.0f ? __builtin_amdgcn_exp2f((ms[i] - big_m) * kLog2e) : 0.0f;
+        big_l = fmaf(ls[i] > 0.0f ? ls[i] : 0.0f, w, big_l);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          sum[j] = fmaf(__uint_as_float(lo[i][j]), w, sum[j]);
+          sum[4 + j] = fmaf(__uint_as_float(hi[i][j]), w, sum[4 + j]);
+        }
+      }
+    }
+    big_l = sum_rows<LPR>(big_l);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum[j] = sum_rows<LPR>(sum[j]);
+    if (r == 0) {
+      const float inv = (splits > 0 && big_l > 0.0f) ? 1.0f / big_l : 0.0f;
+      uint4 o;
+      o.x = pack_bf16x2(sum[0] * inv, sum[1] * inv);
+      o.y = pack_bf16x2(sum[2] * inv, sum[3] * inv);
+      o.z = pack_bf16x2(sum[4] * inv, sum[5] * inv);
+      o.w = pack_bf16x2(sum[6] * inv, sum[7] * inv);
+      store128(p.out + row * D + cpack * kPackElems, o);
+    }
+  }
+}
+
 template <class Sh>
 __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeParams p) {
   constexpr int G = Sh::G, GW = Sh::GW, HG = Sh::HG, LPR = Sh::LPR, RPL = Sh::RPL;
   constexpr int LOADS = Sh::LOADS, KT = Sh::KT, NP = Sh::NP, S = Sh::S;
   constexpr int D = LPR * kPackElems;
 
-  __shared__ int32_t s_rows[kMaxWaves][kWave];
+  __shared__ int32_t s_rows[kMaxWaves][2][kWave];
   __shared__ float s_prob[kMaxWaves][kWave];
   __shared__ float s_ml[kMaxWaves][2][GW];
   __shared__ float s_acc[kMaxWaves][GW][D];
 
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int waves = blockDim.x / kWave;
+  const int wave = wave_uniform(threadIdx.x / kWave);  // scalar: wave-uniform control flow
+  const int waves = wave_uniform(blockDim.x / kWave);
   const int hg = wave % HG;                 // head group of this wave
   const int key_lane = wave / HG;           // key-tile slot among same-group waves
   const int key_lanes = waves / HG;
   const int r = lane / LPR;                 // key row within a load
   const int cpack = lane % LPR;             // 16-byte pack within the row
 
-  const int32_t split = blockIdx.x;
-  const int32_t head = blockIdx.y;
+  const int32_t split = blockIdx.y;  // heads fastest: co-running workgroups read whole token rows
+  const int32_t head = blockIdx.x;
   const int32_t b = blockIdx.z;
   const Gemma4KvCacheConfig &c = p.c;
 
@@ -229,14 +358,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
   const int32_t end = min(seq_len, begin + p.split_size);
 
   // ---- Q for the GW heads of this wave, 8 dims per lane, pre-scaled
-  float qf[GW][8];
+  // Q stays packed bf16 (two dims per register): Q·K runs on v_dot2 with
+  // exact products and fp32 sums; the softmax scale is applied to the sum.
+  uint32_t qw[GW][4];
 #pragma unroll
   for (int g = 0; g < GW; ++g) {
     const int qh = head * G + hg * GW + g;
     const uint4 qp = load128(p.q + ((int64_t)b * kQueryHeads + qh) * D + cpack * kPackElems);
-    unpack8(qp, qf[g]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) qf[g][j] *= p.q_scale;
+    qw[g][0] = qp.x; qw[g][1] = qp.y; qw[g][2] = qp.z; qw[g][3] = qp.w;
   }
 
   // Score-lane identity after the butterfly: one (key, head) per lane.
@@ -257,62 +386,90 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
   const uint16_t *vbase = p.cache_v + (int64_t)head * D + cpack * kPackElems;
   const int64_t new_off = ((int64_t)b * c.num_heads + head) * D + cpack * kPackElems;
 
-  const int32_t n_tiles = (end - begin + KT - 1) / KT;
-  auto lookup = [&](int32_t tile) -> int32_t {
-    const int32_t key = begin + tile * KT + lane;
-    if (lane >= KT || tile >= n_tiles || key >= end) return kRowInvalid;
-    if (key == new_pos) return kRowNewToken;
-    return key_row(c, p.page_table, p.layer, b, key);
+  // This wave's keys: chunks of kWave keys (one page lookup per lane), chunk
+  // ids key_lane, key_lane + key_lanes, ...; each chunk is CT tiles of KT keys.
+  constexpr int CT = Sh::CT;
+  constexpr int CK = CT * KT;  // keys per chunk
+  const int32_t n_keys = end - begin;
+  const int32_t n_chunks = (n_keys + CK - 1) / CK;
+  const int32_t my_chunks =
+      n_chunks > key_lane ? (n_chunks - key_lane + key_lanes - 1) / key_lanes : 0;
+  int32_t my_tiles = 0;
+  if (my_chunks > 0) {
+    const int32_t last_key0 = (key_lane + (my_chunks - 1) * key_lanes) * CK;
+    my_tiles = (my_chunks - 1) * CT + min(CT, (n_keys - last_key0 + KT - 1) / KT);
+  }
+  // Page lookups are split in two so the page-table load can stay in flight
+  // for a whole chunk: fetch_page issues the (always in-bounds) load for the
+  // lane's key of my chunk m; page_row turns it into a cache row, branch-free.
+  const int32_t pt_row = b * c.max_pages_per_seq;
+  auto chunk_key = [&](int32_t m) { return begin + (key_lane + m * key_lanes) * CK + lane; };
+  auto fetch_page = [&](int32_t m) -> int32_t {
+    const int32_t logical_page = chunk_key(m) / c.page_size;
+    return p.page_table[pt_row + logical_page % c.max_pages_per_seq];
+  };
+  auto page_row = [&](int32_t m, int32_t physical) -> int32_t {
+    const int32_t key = chunk_key(m);
+    const int32_t logical_page = key / c.page_size;
+    const bool ok = lane < CK && m < my_chunks && key < end && physical >= 0 &&
+                    physical < c.num_pages;
+    const int32_t row = ((int32_t)p.layer * c.num_pages + physical) * c.page_size +
+                        (key - logical_page * c.page_size);
+    return !ok ? kRowInvalid : (key == new_pos ? kRowNewToken : row);
+  };
+  // Lane l's key goes to slot (tile, r, kl) = (l / KT, l % RPL, (l % KT) / RPL)
+  // so a lane reads its LOADS rows of a tile as one contiguous run.
+  const int table_slot = (lane / KT) * KT + (lane % RPL) * LOADS + (lane % KT) / RPL;
+  auto publish = [&](int32_t m, int32_t row) {
+    if (lane < CK) s_rows[wave][m & 1][table_slot] = row;
+    wave_lds_sync();
   };
 
-  int32_t next_row = lookup(key_lane);
-  for (int32_t tile = key_lane; tile < n_tiles; tile += key_lanes) {
-    // Publish this tile's rows (lane l holds key l) in load order.
-    {
-      const int l = lane;
-      if (l < KT) s_rows[wave][(l % RPL) * LOADS + l / RPL] = next_row;
-    }
-    wave_lds_sync();
+  struct TileBuf {
+    uint4 k[LOADS], v[LOADS];
+    uint32_t valid;
+  };
+  // Issue tile t of my chunk m into `tb`; a tile past the wave's keys is
+  // dead: every row reads as invalid (loads still go out, to cache row 0).
+  auto issue = [&](TileBuf &tb, int32_t m, int t) {
+    const bool live = m * CT + t < my_tiles;
+    const int32_t *rows_p = &s_rows[wave][m & 1][t * KT + r * LOADS];
     int32_t rows[LOADS];
 #pragma unroll
-    for (int kl = 0; kl < LOADS; ++kl) rows[kl] = s_rows[wave][r * LOADS + kl];
-    next_row = lookup(tile + key_lanes);  // overlaps with this tile's loads
-
-    uint4 kraw[LOADS], vraw[LOADS];
-    uint32_t valid_mask = 0;
+    for (int kl = 0; kl < LOADS; ++kl) rows[kl] = live ? rows_p[kl] : kRowInvalid;
+    TileBuf &t_ = tb;
+    // Loads are unconditional (no exec-mask branches, so the wait counters
+    // stay exact across the pipeline); an invalid key reads cache row 0 and
+    // is masked: its score becomes -inf and its V pack zero.
+    t_.valid = 0;
 #pragma unroll
     for (int kl = 0; kl < LOADS; ++kl) {
-      kraw[kl] = make_uint4(0, 0, 0, 0);
-      vraw[kl] = make_uint4(0, 0, 0, 0);
       const int32_t row = rows[kl];
-      if (row != kRowInvalid) {
-        valid_mask |= 1u << kl;
-        const uint16_t *kp = row == kRowNewToken ? p.new_k + new_off
-                                                 : kbase + (int64_t)row * Sh::kRowElems;
-        const uint16_t *vp = row == kRowNewToken ? p.new_v + new_off
-                                                 : vbase + (int64_t)row * Sh::kRowElems;
-        kraw[kl] = load128(kp);
-        vraw[kl] = load128(vp);
-      }
+      t_.valid |= (row != kRowInvalid ? 1u : 0u) << kl;
+      const bool fresh = row == kRowNewToken;
+      const int64_t off = (int64_t)(row < 0 ? 0 : row) * Sh::kRowElems;
+      t_.k[kl] = load128(fresh ? p.new_k + new_off : kbase + off);
+      t_.v[kl] = load128(fresh ? p.new_v + new_off : vbase + off);
     }
+  };
 
+  auto compute = [&](const TileBuf &t) {
     // Partial Q·K over this lane's 8 dims: part[kl * GW + g].
     float part[NP];
 #pragma unroll
     for (int kl = 0; kl < LOADS; ++kl) {
-      float kf[8];
-      unpack8(kraw[kl], kf);
+      const uint32_t kw[4] = {t.k[kl].x, t.k[kl].y, t.k[kl].z, t.k[kl].w};
 #pragma unroll
       for (int g = 0; g < GW; ++g) {
-        float s = 0.0f;
+        float acc_s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) s = fmaf(qf[g][j], kf[j], s);
-        part[kl * GW + g] = s;
+        for (int j = 0; j < 4; ++j) acc_s = dot2_bf16(qw[g][j], kw[j], acc_s);
+        part[kl * GW + g] = acc_s;
       }
     }
     split_butterfly<NP, LPR / 2>(part, lane);
-    const bool valid = (valid_mask >> my_kl) & 1u;
-    const float score = valid ? part[0] : -INFINITY;
+    const bool valid = (t.valid >> my_kl) & 1u;
+    const float score = valid ? part[0] * p.q_scale : -INFINITY;
 
     // Online softmax, once per tile.
     float tmax[GW];
@@ -340,10 +497,9 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
     float pv[NP];
 #pragma unroll
     for (int i = 0; i < NP; i += 4) {
-      const float4 t = *reinterpret_cast<const float4 *>(&s_prob[wave][r * NP + i]);
-      pv[i] = t.x; pv[i + 1] = t.y; pv[i + 2] = t.z; pv[i + 3] = t.w;
+      const float4 q4 = *reinterpret_cast<const float4 *>(&s_prob[wave][r * NP + i]);
+      pv[i] = q4.x; pv[i + 1] = q4.y; pv[i + 2] = q4.z; pv[i + 3] = q4.w;
     }
-
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
 #pragma unroll
@@ -352,12 +508,42 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
 #pragma unroll
     for (int kl = 0; kl < LOADS; ++kl) {
       float vf[8];
-      unpack8(vraw[kl], vf);
+      const bool kl_valid = (t.valid >> kl) & 1u;
+      const uint4 vp = kl_valid ? t.v[kl] : make_uint4(0, 0, 0, 0);
+      unpack8(vp, vf);
 #pragma unroll
       for (int g = 0; g < GW; ++g) {
         const float w = pv[kl * GW + g];
 #pragma unroll
         for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(w, vf[j], acc[g][j]);
+      }
+    }
+  };
+
+  // Software pipeline over my chunks, CT tiles each, fully unrolled inside a
+  // chunk so both register buffers are static: tile t+1's loads are in flight
+  // while tile t computes, and the next chunk's page-table loads are in
+  // flight for a whole chunk. Every load is issued on every path, so the
+  // memory wait counters stay exact.
+  static_assert(CT % 2 == 0, "tiles per chunk alternate between two buffers");
+  if (my_tiles > 0) {
+    publish(0, page_row(0, fetch_page(0)));
+    int32_t next_page = fetch_page(1);
+    TileBuf buf0, buf1;
+    issue(buf0, 0, 0);
+    for (int32_t m = 0; m < my_chunks; ++m) {
+#pragma unroll
+      for (int t = 0; t < CT; t += 2) {
+        issue(buf1, m, t + 1);
+        if (m * CT + t < my_tiles) compute(buf0);
+        if (t + 2 < CT) {
+          issue(buf0, m, t + 2);
+        } else {
+          publish(m + 1, page_row(m + 1, next_page));
+          next_page = fetch_page(m + 2);
+          issue(buf0, m + 1, 0);
+        }
+        if (m * CT + t + 1 < my_tiles) compute(buf1);
       }
     }
   }
@@ -366,15 +552,12 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
   float l_head[GW];
   gather_heads<GW, S>(reduce_sum_from<(1 << S) * GW>(l_lane), my_g, l_head);
 #pragma unroll
-  for (int o = LPR; o < kWave; o <<= 1) {
+  for (int g = 0; g < GW; ++g) {
 #pragma unroll
-    for (int g = 0; g < GW; ++g) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] += xor_lane(acc[g][j], o);
-    }
+    for (int j = 0; j < 8; ++j) acc[g][j] = sum_rows<LPR>(acc[g][j]);
   }
 
-  // ---- combine the waves that share a head group (LDS), then emit
+  // ---- combine the waves that share a head group (LDS)
   if (key_lanes > 1) {
     if (lane == 0) {
 #pragma unroll
@@ -391,68 +574,140 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
       }
     }
     __syncthreads();
-    if (key_lane != 0) return;
+    if (key_lane == 0) {
 #pragma unroll
-    for (int g = 0; g < GW; ++g) {
-      float big_m = -INFINITY;
-      for (int k = 0; k < key_lanes; ++k) big_m = fmaxf(big_m, s_ml[k * HG + hg][0][g]);
-      const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
-      float big_l = 0.0f;
-      float sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      for (int k = 0; k < key_lanes; ++k) {
-        const int w = k * HG + hg;
-        const float f = __builtin_amdgcn_exp2f(s_ml[w][0][g] - m_ref);
-        big_l = fmaf(s_ml[w][1][g], f, big_l);
+      for (int g = 0; g < GW; ++g) {
+        float big_m = -INFINITY;
+        for (int k = 0; k < key_lanes; ++k) big_m = fmaxf(big_m, s_ml[k * HG + hg][0][g]);
+        const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
+        float big_l = 0.0f;
+        float sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int k = 0; k < key_lanes; ++k) {
+          const int w = k * HG + hg;
+          const float f = __builtin_amdgcn_exp2f(s_ml[w][0][g] - m_ref);
+          big_l = fmaf(s_ml[w][1][g], f, big_l);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) sum[j] = fmaf(s_acc[w][g][cpack * 8 + j], f, sum[j]);
+          for (int j = 0; j < 8; ++j) sum[j] = fmaf(s_acc[w][g][cpack * 8 + j], f, sum[j]);
+        }
+        m[g] = big_m;
+        l_head[g] = big_l;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = sum[j];
       }
-      m[g] = big_m;
-      l_head[g] = big_l;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[g][j] = sum[j];
     }
   }
 
-  if (r != 0) return;
+  // ---- emit: the bf16 row when this split is the whole row, else partials
+  const bool emitter = key_lane == 0 && r == 0;
+  // With in-kernel combining, a row with one live split needs no partials.
+  const bool whole_row = direct || (p.counters != nullptr && live_splits == 1);
+  if (emitter) {
 #pragma unroll
-  for (int g = 0; g < GW; ++g) {
-    const int qh = head * G + hg * GW + g;
-    const int64_t row = (int64_t)b * kQueryHeads + qh;
-    if (direct) {
-      const float inv = l_head[g] > 0.0f ? 1.0f / l_head[g] : 0.0f;
-      uint4 o;
-      o.x = pack_bf16x2(acc[g][0] * inv, acc[g][1] * inv);
-      o.y = pack_bf16x2(acc[g][2] * inv, acc[g][3] * inv);
-      o.z = pack_bf16x2(acc[g][4] * inv, acc[g][5] * inv);
-      o.w = pack_bf16x2(acc[g][6] * inv, acc[g][7] * inv);
-      store128(p.out + row * D + cpack * kPackElems, o);
-    } else {
-      const int64_t pidx = row * p.num_splits + split;
-      if (cpack == 0) {
-        p.partial_m[pidx] = m[g] == -INFINITY ? -INFINITY : m[g] * kLn2;
-        p.partial_l[pidx] = l_head[g];
+    for (int g = 0; g < GW; ++g) {
+      const int qh = head * G + hg * GW + g;
+      const int64_t row = (int64_t)b * kQueryHeads + qh;
+      if (whole_row) {
+        const float inv = l_head[g] > 0.0f ? 1.0f / l_head[g] : 0.0f;
+        uint4 o;
+        o.x = pack_bf16x2(acc[g][0] * inv, acc[g][1] * inv);
+        o.y = pack_bf16x2(acc[g][2] * inv, acc[g][3] * inv);
+        o.z = pack_bf16x2(acc[g][4] * inv, acc[g][5] * inv);
+        o.w = pack_bf16x2(acc[g][6] * inv, acc[g][7] * inv);
+        store128(p.out + row * D + cpack * kPackElems, o);
+      } else {
+        const int64_t pidx = row * p.num_splits + split;
+        const float m_nat = m[g] == -INFINITY ? -INFINITY : m[g] * kLn2;
+        if (p.counters != nullptr) {
+          // Device-coherent (sc1) stores: the combining workgroup may run on
+          // another XCD, whose L2 does not see this XCD's write-back lines.
+          if (cpack == 0) {
+            coherent_store(p.partial_m + pidx, m_nat);
+            coherent_store(p.partial_l + pidx, l_head[g]);
+          }
+          coherent_store8(p.partial_acc + pidx * D + cpack * 8, acc[g]);
+        } else {
+          if (cpack == 0) {
+            p.partial_m[pidx] = m_nat;
+            p.partial_l[pidx] = l_head[g];
+          }
+          float4 *dst = reinterpret_cast<float4 *>(p.partial_acc + pidx * D + cpack * 8);
+          dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+          dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+        }
       }
-      float4 *dst = reinterpret_cast<float4 *>(p.partial_acc + pidx * D + cpack * 8);
-      dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
-      dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
     }
   }
+  if (whole_row || p.counters == nullptr) return;
+
+  // ---- in-kernel combine: the last split workgroup of (b, head) to finish
+  // reduces every live split of its GQA heads. The partials went out with
+  // device-coherent stores; each thread waits for its own stores to complete
+  // before the workgroup counts its arrival, so the last arriver's coherent
+  // loads see every split. Whole-L2 write-back/invalidate is never needed.
+  __shared__ int32_t s_last;
+  wait_stores_complete();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t *counter = p.counters + (int64_t)b * c.num_heads + head;
+    const int32_t arrived =
+        __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = arrived == live_splits - 1;
+    if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? 1 : 0;
+  }
+  __syncthreads();
+  if (s_last == 0 || key_lane != 0) return;
+  combine_row_group<GW, D, LPR, RPL>(p, b, head * G + hg * GW, live_splits, r, cpack);
 }
 
 // Log-sum-exp combine of the live splits of one (batch, query head) row
-// (src/gemma4_flash_attention_decode.cu:880-977). One wave per row; each lane
-// owns D/64 consecutive dims.
+// (src/gemma4_flash_attention_decode.cu:880-977), as a separate launch.
+// Workgroup (row, 64-dim block): 256 threads = 16 split lanes x 16 groups of
+// 4 dims. The split maxima come first (all threads, strided over splits); the
+// weights of a chunk of up to kCombineChunk splits go to LDS, every thread
+// accumulates its splits' float4 partials, and the 16 split lanes are summed
+// through LDS.
+constexpr int kCombineThreads = 256;
+constexpr int kCombineChunk = 1024;
+constexpr int kCombineDims = 64;
+
+__device__ __forceinline__ float block_reduce_max(float v, float *s_tmp) {
+  v = reduce_max_from<1>(v);
+  const int wave = threadIdx.x / kWave;
+  __syncthreads();
+  if (__lane_id() == 0) s_tmp[wave] = v;
+  __syncthreads();
+  float r = s_tmp[0];
+#pragma unroll
+  for (int w = 1; w < kCombineThreads / kWave; ++w) r = fmaxf(r, s_tmp[w]);
+  return r;
+}
+__device__ __forceinline__ float block_reduce_sum(float v, float *s_tmp) {
+  v = reduce_sum_from<1>(v);
+  const int wave = threadIdx.x / kWave;
+  __syncthreads();
+  if (__lane_id() == 0) s_tmp[wave] = v;
+  __syncthreads();
+  float r = s_tmp[0];
+#pragma unroll
+  for (int w = 1; w < kCombineThreads / kWave; ++w) r += s_tmp[w];
+  return r;
+}
+
 template <int kDim>
-__global__ __launch_bounds__(kWave) void decode_combine_kernel(
+__global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
     uint16_t *__restrict__ out, const float *__restrict__ partial_m,
     const float *__restrict__ partial_l, const float *__restrict__ partial_acc,
     const int32_t *__restrict__ seq_lengths, int32_t window_size,
     int32_t split_size, int32_t num_splits) {
-  constexpr int kDimsPerLane = kDim / kWave;  // 4 or 8
-  const int lane = threadIdx.x;
+  __shared__ float s_w[kCombineChunk];
+  __shared__ float s_tmp[kCombineThreads / kWave];
+  __shared__ float s_acc[16][kCombineDims];
+  const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
+  const int dim0 = blockIdx.y * kCombineDims;
   const int32_t b = (int32_t)(row / kQueryHeads);
-  const int32_t seq_len = wave_uniform(seq_lengths[b]);
+  const int32_t seq_len = seq_lengths[b];
   int32_t first = window_size > 0 ? seq_len - window_size : 0;
   first = first < 0 ? 0 : first;
   const int32_t key_count = seq_len > first ? seq_len - first : 0;
@@ -461,48 +716,62 @@ __global__ __launch_bounds__(kWave) void decode_combine_kernel(
 
   const float *pm = partial_m + row * num_splits;
   const float *pl = partial_l + row * num_splits;
-  float big_m = -INFINITY;
-  for (int32_t s = lane; s < splits; s += kWave) big_m = fmaxf(big_m, pm[s]);
-  big_m = reduce_max_from<1>(big_m);
-  float big_l = 0.0f;
-  for (int32_t s = lane; s < splits; s += kWave) {
-    const float ls = pl[s];
-    if (ls > 0.0f) big_l = fmaf(ls, __builtin_amdgcn_exp2f((pm[s] - big_m) * kLog2e), big_l);
-  }
-  big_l = reduce_sum_from<1>(big_l);
+  const float *pa = partial_acc + row * num_splits * kDim + dim0;
+  float mloc = -INFINITY;
+  for (int32_t s = t; s < splits; s += kCombineThreads) mloc = fmaxf(mloc, pm[s]);
+  const float big_m = block_reduce_max(mloc, s_tmp);
 
-  float acc[kDimsPerLane];
-#pragma unroll
-  for (int j = 0; j < kDimsPerLane; ++j) acc[j] = 0.0f;
-  const float *pa = partial_acc + row * num_splits * kDim + lane * kDimsPerLane;
-#pragma unroll 4
-  for (int32_t s = 0; s < splits; ++s) {
-    const float ls = pl[s];
-    const float w = ls > 0.0f ? __builtin_amdgcn_exp2f((pm[s] - big_m) * kLog2e) : 0.0f;
-#pragma unroll
-    for (int j = 0; j < kDimsPerLane; j += 4) {
-      const float4 a = *reinterpret_cast<const float4 *>(pa + (int64_t)s * kDim + j);
-      acc[j] = fmaf(a.x, w, acc[j]);
-      acc[j + 1] = fmaf(a.y, w, acc[j + 1]);
-      acc[j + 2] = fmaf(a.z, w, acc[j + 2]);
-      acc[j + 3] = fmaf(a.w, w, acc[j + 3]);
+  const int dg = t % 16;   // 4-dim group
+  const int sl = t / 16;   // split lane
+  float lloc = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int32_t c0 = 0; c0 < splits; c0 += kCombineChunk) {
+    const int32_t cn = min(kCombineChunk, splits - c0);
+    for (int32_t s = t; s < cn; s += kCombineThreads) {
+      const float ls = pl[c0 + s];
+      const float w = ls > 0.0f ? __builtin_amdgcn_exp2f((pm[c0 + s] - big_m) * kLog2e) : 0.0f;
+      s_w[s] = w;
+      lloc = fmaf(ls > 0.0f ? ls : 0.0f, w, lloc);
     }
+    __syncthreads();
+#pragma unroll 4
+    for (int32_t s = sl; s < cn; s += 16) {
+      const float w = s_w[s];
+      if (w != 0.0f) {
+        const float4 a = *reinterpret_cast<const float4 *>(pa + (int64_t)(c0 + s) * kDim + dg * 4);
+        acc.x = fmaf(a.x, w, acc.x);
+        acc.y = fmaf(a.y, w, acc.y);
+        acc.z = fmaf(a.z, w, acc.z);
+        acc.w = fmaf(a.w, w, acc.w);
+      }
+    }
+    __syncthreads();
   }
-  const float inv = (splits > 0 && big_l > 0.0f) ? 1.0f / big_l : 0.0f;
-  uint16_t *o = out + row * kDim + lane * kDimsPerLane;
+  const float big_l = block_reduce_sum(lloc, s_tmp);
+  s_acc[sl][dg * 4 + 0] = acc.x;
+  s_acc[sl][dg * 4 + 1] = acc.y;
+  s_acc[sl][dg * 4 + 2] = acc.z;
+  s_acc[sl][dg * 4 + 3] = acc.w;
+  __syncthreads();
+  if (t < kCombineDims / 4) {
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int j = 0; j < kDimsPerLane; j += 4) {
-    uint2 w;
-    w.x = pack_bf16x2(acc[j] * inv, acc[j + 1] * inv);
-    w.y = pack_bf16x2(acc[j + 2] * inv, acc[j + 3] * inv);
-    *reinterpret_cast<uint2 *>(o + j) = w;
+    for (int k = 0; k < 16; ++k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += s_acc[k][t * 4 + j];
+    }
+    const float inv = (splits > 0 && big_l > 0.0f) ? 1.0f / big_l : 0.0f;
+    uint2 o;
+    o.x = pack_bf16x2(v[0] * inv, v[1] * inv);
+    o.y = pack_bf16x2(v[2] * inv, v[3] * inv);
+    *reinterpret_cast<uint2 *>(out + row * kDim + dim0 + t * 4) = o;
   }
 }
 
-// (8 kv heads x 256): 2 GQA heads per wave, 16 loads -> 32-key tiles.
-using SlidingShape = DecodeShape<8, 256, 2, 16>;
+// (8 kv heads x 256): 2 GQA heads per wave, 8 loads -> 16-key tiles.
+using SlidingShape = DecodeShape<8, 256, 2, 8, 2>;
 // (1 kv head x 512): 16 GQA heads as 4 groups of 4, 8 loads -> 8-key tiles.
-using GlobalRefShape = DecodeShape<1, 512, 4, 8>;
+using GlobalRefShape = DecodeShape<1, 512, 4, 8, 4>;
 
 bool valid_decode_config(const Gemma4KvCacheConfig &c, int32_t layer) {
   const int64_t capacity = (int64_t)c.max_pages_per_seq * c.page_size;
@@ -514,9 +783,9 @@ bool valid_decode_config(const Gemma4KvCacheConfig &c, int32_t layer) {
 
 template <class Sh>
 int waves_for(int32_t split_size) {
-  const int tiles = (split_size + Sh::KT - 1) / Sh::KT;
+  const int chunks = (split_size + Sh::CT * Sh::KT - 1) / (Sh::CT * Sh::KT);
   int key_lanes = 1;
-  while (key_lanes * 2 * Sh::HG <= kMaxWaves && key_lanes < tiles) key_lanes *= 2;
+  while (key_lanes * 2 * Sh::HG <= kMaxWaves && key_lanes < chunks) key_lanes *= 2;
   return key_lanes * Sh::HG;
 }
 
@@ -526,12 +795,13 @@ hipError_t launch_decode(const DecodeParams &p, int32_t batch_count,
   constexpr int D = Sh::LPR * kPackElems;
   const int waves = waves_for<Sh>(p.split_size);
   hipLaunchKernelGGL(decode_split_kernel<Sh>,
-                     dim3(p.num_splits, p.c.num_heads, batch_count),
+                     dim3(p.c.num_heads, p.num_splits, batch_count),
                      dim3(waves * kWave), 0, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.num_splits == 1) return e;
-  hipLaunchKernelGGL(decode_combine_kernel<D>, dim3(batch_count * kQueryHeads),
-                     dim3(kWave), 0, stream, p.out, p.partial_m, p.partial_l,
+  if (e != hipSuccess || p.num_splits == 1 || p.counters != nullptr) return e;
+  hipLaunchKernelGGL(decode_combine_kernel<D>,
+                     dim3(batch_count * kQueryHeads, D / kCombineDims),
+                     dim3(kCombineThreads), 0, stream, p.out, p.partial_m, p.partial_l,
                      p.partial_acc, p.seq_lengths, p.c.window_size, p.split_size,
                      p.num_splits);
   return hipGetLastError();
@@ -541,12 +811,13 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
                         const uint16_t *q, uint16_t *cache_k, uint16_t *cache_v,
                         const int32_t *page_table, const int32_t *seq_lengths,
                         const int32_t *token_position, const uint16_t *new_k,
-                        const uint16_t *new_v, const Gemma4KvCacheConfig &c,
+                        const uint16_t *new_v, int32_t *counters,
+                        const Gemma4KvCacheConfig &c,
                         int32_t layer, float softmax_scale, int32_t split_size,
                         int32_t num_splits, int32_t batch_count,
                         hipStream_t stream) {
   if (batch_count == 0) return hipSuccess;
-  if (batch_count < 0 || batch_count > c.batch_size || batch_count > 65535 ||
+  if (batch_count < 0 || batch_count > c.batch_size || batch_count > 65535 || num_splits > 65535 ||
       !valid_decode_config(c, layer) || !(softmax_scale > 0.0f) ||
       split_size <= 0 || num_splits <= 0 || out == nullptr || q == nullptr ||
       cache_k == nullptr || cache_v == nullptr || page_table == nullptr ||
@@ -567,6 +838,7 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
   p.page_table = page_table;
   p.seq_lengths = seq_lengths;
   p.token_position = token_position;
+  p.counters = num_splits > 1 ? counters : nullptr;
   p.new_k = new_k;
   p.new_v = new_v;
   p.c = c;
@@ -602,7 +874,7 @@ hipError_t gemma4_flash_attention_decode_paged_bf16(
       reinterpret_cast<const uint16_t *>(d_q),
       const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(d_cache_k)),
       const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(d_cache_v)),
-      d_page_table, d_seq_lengths, nullptr, nullptr, nullptr, config, layer,
+      d_page_table, d_seq_lengths, nullptr, nullptr, nullptr, nullptr, config, layer,
       softmax_scale, split_size, num_splits, batch_count, stream);
 }
 
@@ -611,9 +883,10 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
     float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
     gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
     const int32_t *d_seq_lengths, const int32_t *d_token_position,
-    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, Gemma4KvCacheConfig config,
-    int32_t layer, float softmax_scale, int32_t split_size, int32_t num_splits,
-    int32_t batch_count, hipStream_t stream) {
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, int32_t *d_split_counters,
+    Gemma4KvCacheConfig config, int32_t layer, float softmax_scale,
+    int32_t split_size, int32_t num_splits, int32_t batch_count,
+    hipStream_t stream) {
   if (d_token_position == nullptr || d_k == nullptr || d_v == nullptr) {
     return hipErrorInvalidValue;
   }
@@ -622,7 +895,8 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
       reinterpret_cast<const uint16_t *>(d_q), reinterpret_cast<uint16_t *>(d_cache_k),
       reinterpret_cast<uint16_t *>(d_cache_v), d_page_table, d_seq_lengths,
       d_token_position, reinterpret_cast<const uint16_t *>(d_k),
-      reinterpret_cast<const uint16_t *>(d_v), config, layer, softmax_scale,
+      reinterpret_cast<const uint16_t *>(d_v), d_split_counters, config, layer,
+      softmax_scale,
       split_size, num_splits, batch_count, stream);
 }
 
@@ -636,13 +910,14 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
   }
   int32_t tile;
   if (config.num_heads == 8 && config.head_dim == 256) {
-    tile = SlidingShape::KT;
+    tile = SlidingShape::KT * SlidingShape::CT;  // one wave's page-lookup chunk
   } else if (config.num_heads == 1 && config.head_dim == 512) {
-    tile = GlobalRefShape::KT;
+    tile = GlobalRefShape::KT * GlobalRefShape::CT;
   } else {
     return hipErrorInvalidValue;
   }
-  if (target_workgroups <= 0) target_workgroups = 512;  // two per CU on 256 CUs
+  // Default: eight split workgroups per CU; ragged batches need the slack.
+  if (target_workgroups <= 0) target_workgroups = 2048;
   const int64_t keys = (int64_t)std::max(max_live_keys, 1);
   const int64_t heads = (int64_t)batch_count * config.num_heads;
   int64_t splits_per_seq = (target_workgroups + heads - 1) / heads;

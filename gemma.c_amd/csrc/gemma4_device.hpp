@@ -46,9 +46,63 @@ __device__ __forceinline__ void unpack8(const uint4 &p, float (&f)[8]) {
   f[6] = bf16_lo(p.w); f[7] = bf16_hi(p.w);
 }
 
-// Cross-lane exchange within the wave (lane ^ mask).
-__device__ __forceinline__ float xor_lane(float v, int mask) {
-  return __shfl_xor(v, mask, kWave);
+// a.lo*b.lo + a.hi*b.hi + c for packed bf16 pairs (v_dot2c_f32_bf16): the
+// products are exact in fp32 and the sum is rounded once per step.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                        __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// ---- cross-lane exchanges (wave64) ----------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+template <int kMask>
+__device__ __forceinline__ float swizzle_xor(float v) {
+  static_assert(kMask > 0 && kMask < 32, "ds_swizzle bitmask mode works within 32 lanes");
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (kMask << 10)));
+}
+__device__ __forceinline__ float xor_lane32(float v) {
+  const unsigned bits = __builtin_bit_cast(unsigned, v);
+  const auto swapped = __builtin_amdgcn_permlane32_swap(bits, bits, false, false);
+  return __builtin_bit_cast(float, __lane_id() < 32 ? swapped[1] : swapped[0]);
+}
+
+// Value of lane (lane ^ kMask): quad DPP for 1 and 2, ds_swizzle within 32
+// lanes, permlane32 swap across the two halves of the wave.
+template <int kMask>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(kMask > 0 && kMask < kWave, "lane mask");
+  if constexpr (kMask == 1) {
+    return dpp_move<0xB1>(v);  // quad_perm [1,0,3,2]
+  } else if constexpr (kMask == 2) {
+    return dpp_move<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (kMask < 32) {
+    return swizzle_xor<kMask>(v);
+  } else if constexpr (kMask == 32) {
+    return xor_lane32(v);
+  } else {
+    return xor_lane32(swizzle_xor<kMask - 32>(v));
+  }
+}
+
+// Value of a partner lane that differs from this lane in bit kBit and agrees
+// on every higher bit (lower bits may differ); the pairing is an involution.
+// Butterfly sums only need such a pairing, and row mirrors are plain DPP:
+// bit 2 -> row_half_mirror (i <-> 7-i), bit 3 -> row_mirror (i <-> 15-i).
+template <int kBit>
+__device__ __forceinline__ float lane_pair(float v) {
+  if constexpr (kBit == 4) {
+    return dpp_move<0x141>(v);
+  } else if constexpr (kBit == 8) {
+    return dpp_move<0x140>(v);
+  } else {
+    return lane_xor<kBit>(v);
+  }
 }
 
 // Wave-uniform value read from lane 0 (a scalar register after readfirstlane).

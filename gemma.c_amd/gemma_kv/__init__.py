@@ -74,7 +74,7 @@ SIGNATURES = {
     "gemma4_flash_attention_decode_paged_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_flash_attention_append_decode_paged_bf16": (
-        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_decode_split_plan": (_I32, [_CFG, _I32, _I32, _I32, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
 }
 
@@ -199,9 +199,10 @@ def flash_attention_append_decode_paged_bf16(out, partial_m, partial_l, partial_
                                              seq_lengths, token_position, k, v,
                                              config, layer, softmax_scale,
                                              split_size, num_splits, batch_count,
-                                             stream=None) -> int:
+                                             stream=None, split_counters=None) -> int:
     return lib().gemma4_flash_attention_append_decode_paged_bf16(
         ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(q),
         ptr(cache_k), ptr(cache_v), ptr(page_table), ptr(seq_lengths),
-        ptr(token_position), ptr(k), ptr(v), config, layer, softmax_scale,
+        ptr(token_position), ptr(k), ptr(v), ptr(split_counters), config, layer,
+        softmax_scale,
         split_size, num_splits, batch_count, stream_handle(stream))

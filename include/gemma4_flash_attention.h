@@ -51,18 +51,25 @@ hipError_t gemma4_flash_attention_decode_paged_bf16(
 // phases of decode_megakernel_fused_layer_kernel
 // (src/gemma4_flash_attention_decode.cu:306-375, 979-1034) without the
 // RMSNorm/RoPE preparation (K/V arrive prepared).
+// d_token_position[b] must be a live key of sequence b (seq_lengths[b] - 1 in
+// a decode step) or a position whose slot holds no live key.
+// d_split_counters: null -> a second kernel combines the splits; otherwise
+// [batch_count * num_heads] int32, zero before the first call, and the last
+// split workgroup of each (b, kv_head) combines in the same launch and
+// re-arms its counter to zero. Calls sharing a counter array must not overlap.
 hipError_t gemma4_flash_attention_append_decode_paged_bf16(
     gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
     float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
     gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
     const int32_t *d_seq_lengths, const int32_t *d_token_position,
-    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, Gemma4KvCacheConfig config,
-    int32_t layer, float softmax_scale, int32_t split_size, int32_t num_splits,
-    int32_t batch_count, hipStream_t stream);
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, int32_t *d_split_counters,
+    Gemma4KvCacheConfig config, int32_t layer, float softmax_scale,
+    int32_t split_size, int32_t num_splits, int32_t batch_count,
+    hipStream_t stream);
 
 // Split plan for the MI355X: the split size (a multiple of the kernel's key
-// tile) that gives about `target_workgroups` split workgroups (0 = default,
-// two per CU) for `batch_count` sequences of up to `max_live_keys` live keys,
+// wave chunk) that gives about `target_workgroups` split workgroups (0 = default,
+// eight per CU) for `batch_count` sequences of up to `max_live_keys` live keys,
 // and the split count that covers `max_live_keys`. Replaces the fixed
 // GEMMA4_SLIDING_DECODE_SPLIT_SIZE (src/gemma4.h:24) and the active split
 // count of src/gemma4_decode_megakernel.cu:158-167.

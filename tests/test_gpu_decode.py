@@ -17,7 +17,7 @@ pytestmark = pytest.mark.gpu
 
 
 def _run_decode(dev, cfg, q, ck, cv, pt, seq, layer, scale, split_size, num_splits,
-                fused=None):
+                fused=None, counters=None):
     import torch
     batch = len(seq)
     dim = cfg[6]
@@ -37,7 +37,7 @@ def _run_decode(dev, cfg, q, ck, cv, pt, seq, layer, scale, split_size, num_spli
         code = gk.flash_attention_append_decode_paged_bf16(
             out, pm, pl, pa, to_dev(q, dev), ck, cv, to_dev(pt, dev),
             to_dev(np.asarray(seq, np.int32), dev), to_dev(np.asarray(pos, np.int32), dev),
-            to_dev(k_new, dev), to_dev(v_new, dev), **args)
+            to_dev(k_new, dev), to_dev(v_new, dev), split_counters=counters, **args)
     gk.check(code, "decode")
     torch.cuda.synchronize()
     return from_dev_bf16(out)
@@ -150,6 +150,17 @@ def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, wi
     unfused = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, 1 / math.sqrt(dim), split_size,
                           num_splits)
     assert np.array_equal(unfused, got)
+    # In-kernel split combine (self-re-arming counters): same result on three
+    # calls in a row, and the counters end at zero.
+    import torch
+    counters = torch.zeros(batch * heads, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        again = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, 1 / math.sqrt(dim), split_size,
+                            num_splits, fused=(pos, k_new, v_new), counters=counters)
+        assert_close(again, exp, "fused, in-kernel combine")
+        assert np.abs(oracle.bf16_to_f32(again) - oracle.bf16_to_f32(got)).max() <= 2 ** -7
+    assert not counters.cpu().numpy().any()
+    assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
 
 
 def test_split_count_invariance_closed_forms(dev):
