@@ -121,6 +121,14 @@ def launch_layer(gk, L, meta, scratch, stream):
         L.split, L.n_splits, 1, stream=stream, split_counters=None)
 
 
+def launch_split_only(gk, L, meta, scratch, stream):
+    """Phase 1 alone (fused append + split partials): the dominant kernel."""
+    return gk.flash_attention_decode_split_paged_bf16(
+        L.out, scratch["pm"], scratch["pl"], scratch["pa"], L.q, L.ck, L.cv, L.pt,
+        meta["seq"], meta["pos"], L.k, L.v, L.cfg, L.cache_layer, 1.0 / math.sqrt(DIM),
+        L.split, L.n_splits, 1, stream=stream)
+
+
 def time_graph(torch, fn, reps, warmup):
     """Capture fn() once as a HIP graph; replay `reps` times between events."""
     s = torch.cuda.Stream()
@@ -311,24 +319,33 @@ def main():
         torch.cuda.synchronize()
         return
 
-    # ---- dominant kernel: the global-layer launch, live HIP-event timing
+    # ---- per-kernel timing, live with HIP events on the launch stream: the
+    # split phase (fused append + partials) of the global and of the sliding
+    # layers, each replayed back-to-back from a graph.
     g_layers = [L for L in layers if L.is_global]
+    s_layers = [L for L in layers if not L.is_global]
 
-    def global_round(stream):
-        for L in g_layers:
-            gk.check(launch_layer(gk, L, meta, scratch, stream), "global layer")
+    def split_round(Ls):
+        def fn(stream):
+            for L in Ls:
+                gk.check(launch_split_only(gk, L, meta, scratch, stream), "split phase")
+        return fn
 
     if args.only == "global":
         for _ in range(args.steps):
-            global_round(torch.cuda.current_stream().cuda_stream)
+            split_round(g_layers)(torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         return
 
-    g_rounds = 20
-    g_ms, _ = time_graph(torch, lambda st: [global_round(st) for _ in range(g_rounds)], 3, 1)
-    g_launch_us = g_ms * 1e3 / (g_rounds * len(g_layers))
+    rounds = 20
+    g_ms, _ = time_graph(torch, lambda st: [split_round(g_layers)(st) for _ in range(rounds)], 3, 1)
+    s_ms, _ = time_graph(torch, lambda st: [split_round(s_layers)(st) for _ in range(4)], 3, 1)
+    g_launch_us = g_ms * 1e3 / (rounds * len(g_layers))
+    s_launch_us = s_ms * 1e3 / (4 * len(s_layers))
     g_bytes = g_layers[0].bytes
+    s_bytes = s_layers[0].bytes
     g_gbs = g_bytes / (g_launch_us * 1e-6) / 1e9
+    s_gbs = s_bytes / (s_launch_us * 1e-6) / 1e9
     traffic = read_traffic("decode_split_global_ctx8192")
 
     # ---- the headline: full 48-layer step, graph replay and eager
@@ -360,11 +377,15 @@ def main():
         "eager": {"ms_per_step": round(ms_eager, 4),
                   "us_per_layer_step": round(ms_eager * 1e3 / NUM_LAYERS, 3),
                   "achieved_GBs": round(gbs_eager, 1)},
-        "roofline": {"kernel": "decode_split_kernel<8x256> global layer (ctx 8193, fused append+combine)",
+        "roofline": {"kernel": "decode_split_kernel<8x256>, global layer (8193 keys, fused append)",
                      "bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(g_gbs / HBM_PEAK_GBS, 4),
                      "traffic": traffic, "avg_launch_us": round(g_launch_us, 3),
-                     "algorithmic_bytes_per_launch": g_bytes},
+                     "algorithmic_bytes_per_launch": g_bytes,
+                     "split_size": g_layers[0].split, "num_splits": g_layers[0].n_splits},
+        "sliding_split_kernel": {"avg_launch_us": round(s_launch_us, 3), "achieved_GBs": round(s_gbs, 1),
+                                 "algorithmic_bytes_per_launch": s_bytes,
+                                 "split_size": s_layers[0].split, "num_splits": s_layers[0].n_splits},
     }
     if not args.no_batch64:
         b64 = bench_batch64(torch, gk, dev, max(3, args.steps // 5), 2)

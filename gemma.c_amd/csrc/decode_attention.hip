@@ -790,7 +790,7 @@ int waves_for(int32_t split_size) {
 }
 
 template <class Sh>
-hipError_t launch_decode(const DecodeParams &p, int32_t batch_count,
+hipError_t launch_decode(const DecodeParams &p, int32_t batch_count, bool combine,
                          hipStream_t stream) {
   constexpr int D = Sh::LPR * kPackElems;
   const int waves = waves_for<Sh>(p.split_size);
@@ -798,7 +798,7 @@ hipError_t launch_decode(const DecodeParams &p, int32_t batch_count,
                      dim3(p.c.num_heads, p.num_splits, batch_count),
                      dim3(waves * kWave), 0, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.num_splits == 1 || p.counters != nullptr) return e;
+  if (e != hipSuccess || !combine || p.num_splits == 1 || p.counters != nullptr) return e;
   hipLaunchKernelGGL(decode_combine_kernel<D>,
                      dim3(batch_count * kQueryHeads, D / kCombineDims),
                      dim3(kCombineThreads), 0, stream, p.out, p.partial_m, p.partial_l,
@@ -814,7 +814,7 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
                         const uint16_t *new_v, int32_t *counters,
                         const Gemma4KvCacheConfig &c,
                         int32_t layer, float softmax_scale, int32_t split_size,
-                        int32_t num_splits, int32_t batch_count,
+                        int32_t num_splits, int32_t batch_count, bool combine,
                         hipStream_t stream) {
   if (batch_count == 0) return hipSuccess;
   if (batch_count < 0 || batch_count > c.batch_size || batch_count > 65535 || num_splits > 65535 ||
@@ -847,10 +847,10 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
   p.split_size = split_size;
   p.num_splits = num_splits;
   if (c.num_heads == 8 && c.head_dim == 256) {
-    return launch_decode<SlidingShape>(p, batch_count, stream);
+    return launch_decode<SlidingShape>(p, batch_count, combine, stream);
   }
   if (c.num_heads == 1 && c.head_dim == 512) {
-    return launch_decode<GlobalRefShape>(p, batch_count, stream);
+    return launch_decode<GlobalRefShape>(p, batch_count, combine, stream);
   }
   return hipErrorInvalidValue;
 }
@@ -875,7 +875,7 @@ hipError_t gemma4_flash_attention_decode_paged_bf16(
       const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(d_cache_k)),
       const_cast<uint16_t *>(reinterpret_cast<const uint16_t *>(d_cache_v)),
       d_page_table, d_seq_lengths, nullptr, nullptr, nullptr, nullptr, config, layer,
-      softmax_scale, split_size, num_splits, batch_count, stream);
+      softmax_scale, split_size, num_splits, batch_count, /*combine=*/true, stream);
 }
 
 hipError_t gemma4_flash_attention_append_decode_paged_bf16(
@@ -897,7 +897,54 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
       d_token_position, reinterpret_cast<const uint16_t *>(d_k),
       reinterpret_cast<const uint16_t *>(d_v), d_split_counters, config, layer,
       softmax_scale,
-      split_size, num_splits, batch_count, stream);
+      split_size, num_splits, batch_count, /*combine=*/true, stream);
+}
+
+hipError_t gemma4_flash_attention_decode_split_paged_bf16(
+    gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
+    float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+    const int32_t *d_seq_lengths, const int32_t *d_token_position,
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, Gemma4KvCacheConfig config,
+    int32_t layer, float softmax_scale, int32_t split_size, int32_t num_splits,
+    int32_t batch_count, hipStream_t stream) {
+  if (d_token_position != nullptr && (d_k == nullptr || d_v == nullptr)) {
+    return hipErrorInvalidValue;
+  }
+  return decode_entry(
+      reinterpret_cast<uint16_t *>(d_out), d_partial_m, d_partial_l, d_partial_acc,
+      reinterpret_cast<const uint16_t *>(d_q), reinterpret_cast<uint16_t *>(d_cache_k),
+      reinterpret_cast<uint16_t *>(d_cache_v), d_page_table, d_seq_lengths,
+      d_token_position, reinterpret_cast<const uint16_t *>(d_k),
+      reinterpret_cast<const uint16_t *>(d_v), nullptr, config, layer, softmax_scale,
+      split_size, num_splits, batch_count, /*combine=*/false, stream);
+}
+
+hipError_t gemma4_flash_attention_decode_combine_bf16(
+    gemma4_bf16 *d_out, const float *d_partial_m, const float *d_partial_l,
+    const float *d_partial_acc, const int32_t *d_seq_lengths,
+    Gemma4KvCacheConfig config, int32_t split_size, int32_t num_splits,
+    int32_t batch_count, hipStream_t stream) {
+  if (batch_count == 0) return hipSuccess;
+  if (batch_count < 0 || batch_count > 65535 || split_size <= 0 || num_splits <= 0 ||
+      config.window_size < 0 || d_out == nullptr || d_partial_m == nullptr ||
+      d_partial_l == nullptr || d_partial_acc == nullptr || d_seq_lengths == nullptr) {
+    return hipErrorInvalidValue;
+  }
+  uint16_t *out = reinterpret_cast<uint16_t *>(d_out);
+  const dim3 block(kCombineThreads);
+  if (config.head_dim == 256) {
+    hipLaunchKernelGGL(decode_combine_kernel<256>, dim3(batch_count * kQueryHeads, 256 / kCombineDims),
+                       block, 0, stream, out, d_partial_m, d_partial_l, d_partial_acc,
+                       d_seq_lengths, config.window_size, split_size, num_splits);
+  } else if (config.head_dim == 512) {
+    hipLaunchKernelGGL(decode_combine_kernel<512>, dim3(batch_count * kQueryHeads, 512 / kCombineDims),
+                       block, 0, stream, out, d_partial_m, d_partial_l, d_partial_acc,
+                       d_seq_lengths, config.window_size, split_size, num_splits);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,

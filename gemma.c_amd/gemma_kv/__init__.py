@@ -75,6 +75,10 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_flash_attention_append_decode_paged_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
+    "gemma4_flash_attention_decode_split_paged_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
+    "gemma4_flash_attention_decode_combine_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _P]),
     "gemma4_decode_split_plan": (_I32, [_CFG, _I32, _I32, _I32, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
 }
 
@@ -206,3 +210,23 @@ def flash_attention_append_decode_paged_bf16(out, partial_m, partial_l, partial_
         ptr(token_position), ptr(k), ptr(v), ptr(split_counters), config, layer,
         softmax_scale,
         split_size, num_splits, batch_count, stream_handle(stream))
+
+
+def flash_attention_decode_split_paged_bf16(out, partial_m, partial_l, partial_acc, q,
+                                            cache_k, cache_v, page_table, seq_lengths,
+                                            token_position, k, v, config, layer,
+                                            softmax_scale, split_size, num_splits,
+                                            batch_count, stream=None) -> int:
+    return lib().gemma4_flash_attention_decode_split_paged_bf16(
+        ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(q),
+        ptr(cache_k), ptr(cache_v), ptr(page_table), ptr(seq_lengths),
+        ptr(token_position), ptr(k), ptr(v), config, layer, softmax_scale,
+        split_size, num_splits, batch_count, stream_handle(stream))
+
+
+def flash_attention_decode_combine_bf16(out, partial_m, partial_l, partial_acc,
+                                        seq_lengths, config, split_size, num_splits,
+                                        batch_count, stream=None) -> int:
+    return lib().gemma4_flash_attention_decode_combine_bf16(
+        ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(seq_lengths),
+        config, split_size, num_splits, batch_count, stream_handle(stream))

@@ -67,6 +67,28 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
     int32_t split_size, int32_t num_splits, int32_t batch_count,
     hipStream_t stream);
 
+// The two phases of gemma4_flash_attention_decode_paged_bf16 as separate
+// launches, for callers that schedule them apart (or time them): the split
+// phase (phase_decode_paged_grouped_split,
+// src/gemma4_flash_attention_decode.cu:691-878), with the fused append of
+// gemma4_flash_attention_append_decode_paged_bf16 when d_token_position is not
+// null; with num_splits == 1 it writes d_out directly. The combine phase
+// (phase_decode_paged_reduce, src/gemma4_flash_attention_decode.cu:880-977)
+// reduces the live splits of every (batch, query head) row into d_out.
+hipError_t gemma4_flash_attention_decode_split_paged_bf16(
+    gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
+    float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+    const int32_t *d_seq_lengths, const int32_t *d_token_position,
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, Gemma4KvCacheConfig config,
+    int32_t layer, float softmax_scale, int32_t split_size, int32_t num_splits,
+    int32_t batch_count, hipStream_t stream);
+hipError_t gemma4_flash_attention_decode_combine_bf16(
+    gemma4_bf16 *d_out, const float *d_partial_m, const float *d_partial_l,
+    const float *d_partial_acc, const int32_t *d_seq_lengths,
+    Gemma4KvCacheConfig config, int32_t split_size, int32_t num_splits,
+    int32_t batch_count, hipStream_t stream);
+
 // Split plan for the MI355X: the split size (a multiple of the kernel's key
 // wave chunk) that gives about `target_workgroups` split workgroups (0 = default,
 // eight per CU) for `batch_count` sequences of up to `max_live_keys` live keys,

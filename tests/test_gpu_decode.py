@@ -248,3 +248,57 @@ def test_decode_error_convention(dev):
     assert f(buf, None, None, None, buf, buf, buf, idx, idx, small_ring, 0, 0.0625, 32, 1, 1) == inval
     odd = gk.make_config(40, 1024, 1, 1024, 1, 4, 128, 1024)  # unsupported geometry
     assert f(buf, None, None, None, buf, buf, buf, idx, idx, odd, 0, 0.0625, 32, 1, 1) == inval
+
+
+@pytest.mark.parametrize("heads,dim,page,window,seq,split_size,num_splits", [
+    (8, 256, 1, 1024, [3000], 64, 16),
+    (8, 256, 64, 0, [4096, 700], 256, 16),
+    (1, 512, 64, 0, [300, 4100], 128, 33),
+])
+def test_split_and_combine_phases(dev, heads, dim, page, window, seq, split_size, num_splits):
+    """Phase 1 partials match the oracle's split partials (m in natural-log
+    units, l, unnormalised acc: the reference layout), and phase 2 reproduces
+    the one-call result bit for bit."""
+    import torch
+    rng = np.random.default_rng(len(seq) * 17 + split_size)
+    batch = len(seq)
+    max_pages = ring_pages(window, page) if window else (max(seq) + page - 1) // page
+    cfg = cache_config(1, batch, page, max_pages, heads, dim, window)
+    pt = fill_page_table(cfg, seq)
+    n_rows = batch * max_pages * page
+    ck = randn_bf16(rng, (n_rows, heads, dim))
+    cv = randn_bf16(rng, (n_rows, heads, dim))
+    q = randn_bf16(rng, (batch, 16, dim))
+    scale = 1 / math.sqrt(dim)
+    c = gk.make_config(*cfg)
+    rows = batch * 16 * num_splits
+    pm = torch.full((rows,), float("nan"), device=dev)
+    pl = torch.full((rows,), float("nan"), device=dev)
+    pa = torch.full((rows * dim,), float("nan"), device=dev)
+    out = empty_bf16((batch, 16, dim), dev)
+    dq, dck, dcv = to_dev(q, dev), to_dev(ck, dev), to_dev(cv, dev)
+    dpt, dseq = to_dev(pt, dev), to_dev(np.asarray(seq, np.int32), dev)
+    gk.check(gk.flash_attention_decode_split_paged_bf16(
+        out, pm, pl, pa, dq, dck, dcv, dpt, dseq, None, None, None, c, 0, scale,
+        split_size, num_splits, batch))
+    torch.cuda.synchronize()
+    om, ol, oa = oracle.decode_split(q, ck, cv, pt, seq, cfg, 0, scale, split_size, num_splits)
+    gm, gl, ga = pm.cpu().numpy(), pl.cpu().numpy(), pa.cpu().numpy()
+    live = ~np.isnan(om)
+    assert np.array_equal(live, ~np.isnan(gm)), "live split set differs"
+    assert np.allclose(gm[live], om[live], rtol=1e-4, atol=1e-4)
+    # l and acc are relative to each split's own maximum: compare normalised.
+    assert np.allclose(gl[live], ol[live], rtol=2e-3, atol=1e-5)
+    d = dim
+    for i in np.nonzero(live)[0]:
+        if ol[i] > 0:
+            np.testing.assert_allclose(ga[i * d:(i + 1) * d] / gl[i], oa[i * d:(i + 1) * d] / ol[i],
+                                       atol=2e-3, rtol=2e-3)
+    gk.check(gk.flash_attention_decode_combine_bf16(out, pm, pl, pa, dseq, c, split_size,
+                                                    num_splits, batch))
+    torch.cuda.synchronize()
+    two_phase = from_dev_bf16(out)
+    one_call = _run_decode(dev, cfg, q, dck, dcv, pt, seq, 0, scale, split_size, num_splits)
+    assert np.array_equal(two_phase, one_call)
+    exp = oracle.decode_combine(om, ol, oa, seq, cfg, split_size, num_splits)
+    assert_close(two_phase, exp, "combine of oracle partials")
