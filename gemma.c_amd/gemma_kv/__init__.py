@@ -79,6 +79,15 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_flash_attention_decode_combine_bf16": (
         _I32, [_P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _P]),
+    "gemma4_runtime_create": (_I32, [ctypes.POINTER(_P), _I32, _I32, _I32, _P]),
+    "gemma4_runtime_destroy": (None, [_P]),
+    "gemma4_runtime_prefill": (_I32, [_P, _I32, _P]),
+    "gemma4_runtime_decode_step": (_I32, [_P, _P]),
+    "gemma4_runtime_get_config": (_I32, [_P, _I32, ctypes.POINTER(_CFG)]),
+    "gemma4_runtime_get_scalars": (_I32, [_P, ctypes.POINTER(_I32)]),
+    "gemma4_runtime_get_host_vector": (_I32, [_P, _I32, _P, _I64, ctypes.POINTER(_I64)]),
+    "gemma4_runtime_set_host_seq_lengths": (_I32, [_P, _P, _I64]),
+    "gemma4_runtime_device_ptr": (_P, [_P, _I32]),
     "gemma4_decode_split_plan": (_I32, [_CFG, _I32, _I32, _I32, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
 }
 
@@ -230,3 +239,66 @@ def flash_attention_decode_combine_bf16(out, partial_m, partial_l, partial_acc,
     return lib().gemma4_flash_attention_decode_combine_bf16(
         ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(seq_lengths),
         config, split_size, num_splits, batch_count, stream_handle(stream))
+
+
+class Runtime:
+    """Owner of a Gemma4RuntimeState (caches, page tables, token metadata),
+    mirroring src/gemma4_runtime.cuh through the opaque-handle C-ABI."""
+
+    HOST = {"sliding_page_table": 0, "global_page_table": 1, "sliding_slot_logical_pages": 2,
+            "global_slot_logical_pages": 3, "seq_lengths": 4, "token_batch": 5,
+            "token_position": 6}
+    DEVICE = {"sliding_cache_k": 0, "sliding_cache_v": 1, "global_cache_k": 2,
+              "global_cache_v": 3, "sliding_page_table": 4, "global_page_table": 5,
+              "seq_lengths": 6, "token_batch": 7, "token_position": 8, "sliding_cos": 9,
+              "sliding_sin": 10, "global_cos": 11, "global_sin": 12}
+
+    def __init__(self, batch_size, max_seq_len, page_size, stream=None):
+        self._h = ctypes.c_void_p()
+        self.init_code = lib().gemma4_runtime_create(ctypes.byref(self._h), batch_size,
+                                                     max_seq_len, page_size, stream_handle(stream))
+
+    def close(self):
+        if self._h:
+            lib().gemma4_runtime_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def prepare_prefill(self, seq_len, stream=None) -> int:
+        return lib().gemma4_runtime_prefill(self._h, seq_len, stream_handle(stream))
+
+    def prepare_decode_step(self, stream=None) -> int:
+        return lib().gemma4_runtime_decode_step(self._h, stream_handle(stream))
+
+    def config(self, global_cache: bool) -> Gemma4KvCacheConfig:
+        c = Gemma4KvCacheConfig()
+        check(lib().gemma4_runtime_get_config(self._h, int(global_cache), ctypes.byref(c)))
+        return c
+
+    def scalars(self):
+        out = (_I32 * 4)()
+        check(lib().gemma4_runtime_get_scalars(self._h, out))
+        return dict(zip(("batch_size", "max_seq_len", "page_size", "token_count"), list(out)))
+
+    def host(self, name):
+        import numpy as np
+        size = _I64()
+        check(lib().gemma4_runtime_get_host_vector(self._h, self.HOST[name], None, 0,
+                                                   ctypes.byref(size)))
+        arr = np.zeros(size.value, dtype=np.int32)
+        check(lib().gemma4_runtime_get_host_vector(self._h, self.HOST[name], arr.ctypes.data,
+                                                   arr.size, ctypes.byref(size)))
+        return arr
+
+    def set_host_seq_lengths(self, values):
+        import numpy as np
+        arr = np.ascontiguousarray(values, dtype=np.int32)
+        check(lib().gemma4_runtime_set_host_seq_lengths(self._h, arr.ctypes.data, arr.size))
+
+    def device_ptr(self, name) -> int:
+        return lib().gemma4_runtime_device_ptr(self._h, self.DEVICE[name]) or 0
