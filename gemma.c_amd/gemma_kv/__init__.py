@@ -79,6 +79,8 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_flash_attention_decode_combine_bf16": (
         _I32, [_P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _P]),
+    "gemma4_flash_attention_prefill_chunk_paged_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _F32, _P]),
     "gemma4_runtime_create": (_I32, [ctypes.POINTER(_P), _I32, _I32, _I32, _P]),
     "gemma4_runtime_destroy": (None, [_P]),
     "gemma4_runtime_prefill": (_I32, [_P, _I32, _P]),
@@ -302,3 +304,12 @@ class Runtime:
 
     def device_ptr(self, name) -> int:
         return lib().gemma4_runtime_device_ptr(self._h, self.DEVICE[name]) or 0
+
+
+def flash_attention_prefill_chunk_paged_bf16(out, q, k, v, cache_k, cache_v, page_table,
+                                             prior_lengths, config, layer, batch_size,
+                                             chunk_len, softmax_scale, stream=None) -> int:
+    return lib().gemma4_flash_attention_prefill_chunk_paged_bf16(
+        ptr(out), ptr(q), ptr(k), ptr(v), ptr(cache_k), ptr(cache_v), ptr(page_table),
+        ptr(prior_lengths), config, layer, batch_size, chunk_len, softmax_scale,
+        stream_handle(stream))

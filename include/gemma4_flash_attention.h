@@ -89,6 +89,29 @@ hipError_t gemma4_flash_attention_decode_combine_bf16(
     Gemma4KvCacheConfig config, int32_t split_size, int32_t num_splits,
     int32_t batch_count, hipStream_t stream);
 
+// Causal GQA prefill attention of a chunk of `chunk_len` new rows per
+// sequence with bf16 MFMA. Chunk row r of sequence b sits at absolute position
+// P_b + r, P_b = d_prior_lengths[b]; it attends to keys
+// [max(0, pos - window + 1), pos] (window = config.window_size, 0 = no
+// window): keys at positions >= P_b come from the chunk's own prepared
+// d_k/d_v [batch][chunk_len][num_heads][head_dim], earlier keys from the paged
+// cache through the page table (unmapped pages are skipped). The cache is
+// only read: the caller writes the chunk afterwards
+// (gemma4_kv_cache_write_prefill_bf16), as the reference writes after
+// attention (src/gemma4_prefill_megakernel.cu:171-207). d_prior_lengths ==
+// null means plain self-attention of the chunk (the reference launchers'
+// seqlen_q == seqlen_k case) and the cache arguments are ignored.
+// q/out: [batch][chunk_len][16][head_dim]. Geometry: 8 kv heads x 256.
+// Replaces gemma4_flash_fwd_bf16_kernel
+// (src/gemma4_flash_attention_prefill.cu:767-954) and lifts its
+// seqlen_q == seqlen_k restriction (:1131, :1205).
+hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
+    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_v, const gemma4_bf16 *d_cache_k, const gemma4_bf16 *d_cache_v,
+    const int32_t *d_page_table, const int32_t *d_prior_lengths, Gemma4KvCacheConfig config,
+    int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
+    hipStream_t stream);
+
 // Split plan for the MI355X: the split size (a multiple of the kernel's key
 // wave chunk) that gives about `target_workgroups` split workgroups (0 = default,
 // eight per CU) for `batch_count` sequences of up to `max_live_keys` live keys,
