@@ -63,7 +63,7 @@ template <int D>
 struct PrefillSmem {
   uint16_t k[2][kKeyTile][D + kKPad];
   uint16_t vt[2][D][kKeyTile + kVPad];
-  int32_t valid[2][kKeyTile];
+  alignas(16) int32_t valid[2][kKeyTile];
 };
 
 template <int D>
@@ -113,51 +113,91 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int tile0 = (kstart / kKeyTile) * kKeyTile;
   const int n_tiles = wg_last < tile0 ? 0 : (wg_last - tile0) / kKeyTile + 1;
 
-  // Source row of one key for this head: cache (prior keys) or chunk; null if
-  // out of range or on an unmapped page.
-  const Gemma4KvCacheConfig &c = p.c;
-  auto key_src = [&](int kp, const uint16_t *cache, const uint16_t *chunk) -> const uint16_t * {
-    if (kp < 0 || kp > wg_last) return nullptr;
-    if (kp >= prior) return chunk + (((int64_t)b * Lq + (kp - prior)) * Hk + head) * D;
-    if (cache == nullptr) return nullptr;
-    const int lp = kp / c.page_size;
-    const int phys = p.page_table[b * c.max_pages_per_seq + lp % c.max_pages_per_seq];
-    if (phys < 0 || phys >= c.num_pages) return nullptr;
-    const int64_t crow = ((int64_t)p.layer * c.num_pages + phys) * c.page_size + (kp - lp * c.page_size);
-    return cache + (crow * Hk + head) * D;
-  };
-
   // Staging assignment. K: thread t copies 16-B part (t % 32) of keys
   // t/32 + 8i. V: thread t transposes keys 4*(t%8)..+3 x dims 8*(t/8)..+7.
+  // Thread-local key j (0..3 for K, 4..7 for V) of a tile at kt:
   const int kpart = t % 32;
   const int vkg = t % 8;
   const int vdg = t / 8;
+  auto tile_key = [&](int j) { return j < 4 ? t / 32 + 8 * j : 4 * vkg + (j - 4); };
+
+  // Page lookups run two tiles ahead of the MFMAs: fetch_pages issues the
+  // page-table loads of a tile's prior keys; issue_tile turns them into
+  // source rows and issues the K/V loads of the next tile. Every load is
+  // unconditional (a harmless in-bounds word / dummy row when there is
+  // nothing to read) so no divergent branch disturbs the wait counters.
+  const Gemma4KvCacheConfig &c = p.c;
+  const bool paged = p.page_table != nullptr && prior > 0;
+  const float inv_page = 1.0f / (float)c.page_size;
+  auto page_of = [&](int kp) {  // kp / page_size for 0 <= kp < 2^24
+    int lp = (int)((float)kp * inv_page);
+    lp += (lp + 1) * c.page_size <= kp ? 1 : 0;
+    lp -= lp * c.page_size > kp ? 1 : 0;
+    return lp;
+  };
+  const int32_t *pt_row = paged ? p.page_table + b * c.max_pages_per_seq
+                                : reinterpret_cast<const int32_t *>(p.q);
+  const int pt_mod = paged ? c.max_pages_per_seq : 1;
+  auto fetch_pages = [&](int kt, int32_t (&pg)[8]) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int kp = kt + tile_key(j);
+      kp = kp < prior ? kp : prior - 1;  // chunk keys: any in-bounds slot
+      kp = kp < 0 ? 0 : kp;
+      pg[j] = pt_row[page_of(kp) % pt_mod];
+    }
+  };
+  // Element offset of one key's row for this head, or -1 when the key is out
+  // of the workgroup's range or on an unmapped page; cache rows carry bit 62.
+  constexpr int64_t kCacheBit = 1ll << 62;
+  auto key_off = [&](int kp, int phys) -> int64_t {
+    const int64_t chunk_off = (((int64_t)b * Lq + (kp - prior)) * Hk + head) * D;
+    const int lp = page_of(kp < 0 ? 0 : kp);
+    const int64_t crow = ((int64_t)p.layer * c.num_pages + phys) * c.page_size + (kp - lp * c.page_size);
+    const int64_t cache_off = ((crow * Hk + head) * D) | kCacheBit;
+    const bool in_range = kp >= 0 && kp <= wg_last;
+    const bool cached_ok = paged && phys >= 0 && phys < c.num_pages;
+    const int64_t off = kp >= prior ? chunk_off : (cached_ok ? cache_off : -1);
+    return in_range ? off : -1;
+  };
+  auto src_of = [&](int64_t off, const uint16_t *cache, const uint16_t *chunk) {
+    const uint16_t *base = (off & kCacheBit) ? cache : chunk;
+    return off < 0 ? chunk : base + (off & ~kCacheBit);  // invalid: dummy row, masked later
+  };
+
   struct Stage {
     uint4 k[KCH];
     uint4 v[4];
+    uint32_t valid;  // bit i: K key t/32 + 8i valid; bit 4+i: V key 4*(t%8)+i valid
   };
-  auto load_tile = [&](Stage &st, int kt) {
+  auto issue_tile = [&](Stage &st, int kt, const int32_t (&pg)[8]) {
+    st.valid = 0;
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      const int key = t / 32 + 8 * i;
-      const uint16_t *src = key_src(kt + key, p.cache_k, p.k);
-      st.k[i] = src != nullptr ? load128(src + kpart * 8) : make_uint4(0, 0, 0, 0);
+      const int64_t off = key_off(kt + tile_key(i), pg[i]);
+      st.valid |= (off >= 0 ? 1u : 0u) << i;
+      st.k[i] = load128(src_of(off, p.cache_k, p.k) + kpart * 8);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint16_t *src = key_src(kt + 4 * vkg + i, p.cache_v, p.v);
-      st.v[i] = src != nullptr ? load128(src + vdg * 8) : make_uint4(0, 0, 0, 0);
+      const int64_t off = key_off(kt + tile_key(4 + i), pg[4 + i]);
+      st.valid |= (off >= 0 ? 1u : 0u) << (4 + i);
+      st.v[i] = load128(src_of(off, p.cache_v, p.v) + vdg * 8);
     }
   };
   auto store_tile = [&](const Stage &st, int buf) {
 #pragma unroll
     for (int i = 0; i < KCH; ++i) {
-      store128(&sm.k[buf][t / 32 + 8 * i][kpart * 8], st.k[i]);
+      const bool ok = (st.valid >> i) & 1u;
+      store128(&sm.k[buf][t / 32 + 8 * i][kpart * 8], ok ? st.k[i] : make_uint4(0, 0, 0, 0));
+      if (kpart == 0) sm.valid[buf][t / 32 + 8 * i] = ok ? 1 : 0;
     }
-    const uint32_t w[4][4] = {{st.v[0].x, st.v[0].y, st.v[0].z, st.v[0].w},
-                              {st.v[1].x, st.v[1].y, st.v[1].z, st.v[1].w},
-                              {st.v[2].x, st.v[2].y, st.v[2].z, st.v[2].w},
-                              {st.v[3].x, st.v[3].y, st.v[3].z, st.v[3].w}};
+    uint32_t w[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 vv = ((st.valid >> (4 + i)) & 1u) ? st.v[i] : make_uint4(0, 0, 0, 0);
+      w[i][0] = vv.x; w[i][1] = vv.y; w[i][2] = vv.z; w[i][3] = vv.w;
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
@@ -166,10 +206,6 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
       pair.y = __builtin_amdgcn_perm(w[3][e / 2], w[2][e / 2], sel);
       *reinterpret_cast<uint2 *>(&sm.vt[buf][vdg * 8 + e][4 * vkg]) = pair;
     }
-  };
-  // Validity of every key of a tile (32 flags), written by threads 0..31.
-  auto store_valid = [&](int kt, int buf) {
-    if (t < kKeyTile) sm.valid[buf][t] = key_src(kt + t, p.cache_k, p.k) != nullptr;
   };
 
   // Online softmax state: lane's row; lanes l and l^32 share a row.
@@ -180,10 +216,12 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   for (int d = 0; d < DB; ++d) acc[d] = f32x16_t{};
 
   Stage st;
+  int32_t pages[8];
   if (n_tiles > 0) {
-    load_tile(st, tile0);
+    fetch_pages(tile0, pages);
+    issue_tile(st, tile0, pages);
+    fetch_pages(tile0 + kKeyTile, pages);
     store_tile(st, 0);
-    store_valid(tile0, 0);
   }
   __syncthreads();
 
@@ -191,24 +229,35 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     const int buf = it & 1;
     const int kt = tile0 + it * kKeyTile;
     const bool more = it + 1 < n_tiles;
-    if (more) load_tile(st, kt + kKeyTile);  // in flight during this tile's MFMAs
-
-    // S^T[key m][row n] = sum_d K[m][d] Q[n][d]
-    f32x16_t s_acc = f32x16_t{};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const uint4 kf = *reinterpret_cast<const uint4 *>(&sm.k[buf][n][16 * s + 8 * half]);
-      s_acc = mfma32(kf, qreg[s], s_acc);
+    if (more) {
+      issue_tile(st, kt + kKeyTile, pages);              // in flight during the MFMAs
+      fetch_pages(kt + 2 * kKeyTile, pages);             // two tiles ahead
     }
+
+    // S^T[key m][row n] = sum_d K[m][d] Q[n][d], as two independent chains.
+    f32x16_t s_even = f32x16_t{}, s_odd = f32x16_t{};
+#pragma unroll
+    for (int s = 0; s < KS; s += 2) {
+      const uint4 k0 = *reinterpret_cast<const uint4 *>(&sm.k[buf][n][16 * s + 8 * half]);
+      const uint4 k1 = *reinterpret_cast<const uint4 *>(&sm.k[buf][n][16 * s + 16 + 8 * half]);
+      s_even = mfma32(k0, qreg[s], s_even);
+      s_odd = mfma32(k1, qreg[s + 1], s_odd);
+    }
+    const f32x16_t s_acc = s_even + s_odd;
     // Lane holds keys m = (i/4)*8 + 4*half + i%4, i = 0..15, of row n.
+    int flags[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int4 f = *reinterpret_cast<const int4 *>(&sm.valid[buf][8 * j + 4 * half]);
+      flags[4 * j] = f.x; flags[4 * j + 1] = f.y; flags[4 * j + 2] = f.z; flags[4 * j + 3] = f.w;
+    }
+    const int win_lo = p.window > 0 ? qpos - p.window : -1;  // visible: win_lo < kp <= qpos
     float sc[16];
     float tmax = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int m = (i / 4) * 8 + 4 * half + (i % 4);
-      const int kp = kt + m;
-      const bool vis = row_ok && sm.valid[buf][m] && kp <= qpos &&
-                       (p.window == 0 || kp > qpos - p.window);
+      const int kp = kt + (i / 4) * 8 + 4 * half + (i % 4);
+      const bool vis = row_ok & (flags[i] != 0) & (kp <= qpos) & (kp > win_lo);
       sc[i] = vis ? s_acc[i] * p.q_scale : -INFINITY;
       tmax = fmaxf(tmax, sc[i]);
     }
@@ -236,18 +285,18 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const uint4 pb = make_uint4(pw[4 * s2], pw[4 * s2 + 1], pw[4 * s2 + 2], pw[4 * s2 + 3]);
+      uint4 vf[DB];  // all fragments of this k-step first: one LDS wait, then DB MFMAs
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
         const uint16_t *vrow = &sm.vt[buf][32 * d + n][16 * s2 + 4 * half];
         const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
         const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 8);
-        acc[d] = mfma32(make_uint4(lo.x, lo.y, hi.x, hi.y), pb, acc[d]);
+        vf[d] = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
+#pragma unroll
+      for (int d = 0; d < DB; ++d) acc[d] = mfma32(vf[d], pb, acc[d]);
     }
-    if (more) {
-      store_tile(st, buf ^ 1);
-      store_valid(kt + kKeyTile, buf ^ 1);
-    }
+    if (more) store_tile(st, buf ^ 1);
     __syncthreads();
   }
 
