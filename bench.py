@@ -5,14 +5,18 @@ Workload: one full-depth batch-1 decode step = 48 layers in
 gemma4 order (40 sliding layers with 1024-slot rings, page 1; 8 global layers,
 page 64), 8 KV heads x 256, 16 query heads, bf16, context 8192 prefilled with
 N(0,1) K/V. Each layer appends the current token (position 8192) and attends
-over its live keys with one fused HIP launch (append + split-K attention +
-in-kernel split combine). Every timed step does the full work; the appended
-position is the same each step so the per-step work is constant.
+over its live keys. The step runs as one persistent launch
+(gemma4_decode_step_layers_bf16) that walks the 48 layers in order; layer i
+reads its q/k/v only after layer i-1's output is complete. Every timed step
+does the full work; the appended position is the same each step so the
+per-step work is constant.
 
-`value` = algorithmic HBM bytes of a step / step time (graph-replayed), with
-all inputs resident in HBM. Also reported: the eager per-launch rate, the
-batch-64 global-layer rate, the roofline of the dominant
-kernel measured live with HIP events, and the CPU oracle baseline.
+`value` = algorithmic HBM bytes of a step / step time, with all inputs
+resident in HBM. Also reported: the per-layer-launch path (48 fused launches
+replayed from a hipGraph), the per-launch split kernels, the batch-64
+global-layer rate, the config-5 prefill chunk (TFLOP/s and
+MFMA utilisation), the roofline of the dominant kernel measured live with HIP
+events, and the CPU oracle baseline.
 """
 from __future__ import annotations
 
@@ -30,6 +34,7 @@ sys.path.insert(0, str(REPO / "gemma.c_amd"))
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 NUM_LAYERS = 48
 HEADS, DIM, QH = 8, 256, 16
 CONTEXT = 8192
@@ -151,6 +156,73 @@ def time_graph(torch, fn, reps, warmup):
     stop.record()
     stop.synchronize()
     return start.elapsed_time(stop) / reps, g
+
+
+class StepRunner:
+    """The whole config-2 step as one persistent launch."""
+
+    def __init__(self, torch, gk, dev, layers, caches, meta):
+        self.gk = gk
+        self.q = torch.stack([L.q for L in layers])
+        self.k = torch.stack([L.k for L in layers])
+        self.v = torch.stack([L.v for L in layers])
+        self.out = torch.zeros((NUM_LAYERS, 1, QH, DIM), dtype=torch.int16, device=dev)
+        self.s_cfg = next(L.cfg for L in layers if not L.is_global)
+        self.g_cfg = next(L.cfg for L in layers if L.is_global)
+        self.caches, self.meta = caches, meta
+        nbytes = gk.decode_step_workspace_bytes(1)
+        self.ws = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+        gk.check(gk.decode_step_workspace_init(self.ws, 1), "decode_step_workspace_init")
+
+    def __call__(self, stream):
+        c, m = self.caches, self.meta
+        self.gk.check(self.gk.decode_step_layers_bf16(
+            self.out, self.q, self.k, self.v, c["sk"], c["sv"], m["s_pt"], self.s_cfg,
+            c["gk"], c["gv"], m["g_pt"], self.g_cfg, m["seq"], m["pos"], 0, NUM_LAYERS,
+            1.0 / math.sqrt(DIM), 1, self.ws, stream=stream), "decode_step_layers")
+
+    def status(self):
+        return self.gk.decode_step_status(self.ws)
+
+
+def bench_prefill(torch, gk, dev, reps):
+    """a 2048-row prefill chunk on one sliding layer (window
+    1024, 1024-slot page-1 ring after a 1536-token prior) and one global layer
+    (prior 6144, page 64); bf16 MFMA QK^T and PV. FLOPs = 4*D per (query row,
+    query head, visible key)."""
+    import numpy as np
+    lq = 2048
+    res = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+    for kind, window, page, prior in (("sliding", WINDOW, 1, 1536), ("global", 0, GLOBAL_PAGE, 6144)):
+        max_pages = WINDOW if window else (prior + lq) // page
+        cfg = gk.make_config(1, max_pages, page, max_pages, 1, HEADS, DIM, window)
+        rows = max_pages * page
+
+        def rnd(shape):
+            return torch.randn(shape, generator=gen, device=dev).bfloat16().view(torch.int16)
+
+        ck, cv = rnd((rows, HEADS, DIM)), rnd((rows, HEADS, DIM))
+        q, k, v = rnd((1, lq, QH, DIM)), rnd((1, lq, HEADS, DIM)), rnd((1, lq, HEADS, DIM))
+        pt = torch.arange(max_pages, dtype=torch.int32, device=dev)
+        out = torch.zeros((1, lq, QH, DIM), dtype=torch.int16, device=dev)
+        pr = torch.tensor([prior], dtype=torch.int32, device=dev)
+
+        def fn(st):
+            gk.check(gk.flash_attention_prefill_chunk_paged_bf16(
+                out, q, k, v, ck, cv, pt, pr, cfg, 0, 1, lq, 1 / 16, stream=st), "prefill")
+
+        ms, _ = time_graph(torch, fn, reps, 3)
+        keys = np.arange(lq) + prior + 1
+        if window:
+            keys = np.minimum(keys, window)
+        flops = 4 * DIM * QH * int(keys.sum())
+        tflops = flops / (ms * 1e-3) / 1e12
+        res[kind] = {"us_per_chunk": round(ms * 1e3, 2), "gflop": round(flops / 1e9, 2),
+                     "tflops": round(tflops, 1),
+                     "mfma_util_vs_bf16_dense_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+    return res
 
 
 def time_eager(torch, fn, reps, warmup):
@@ -280,7 +352,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch64", action="store_true")
-    ap.add_argument("--only", choices=["step", "global", "copy"], default=None,
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill"],
+                    default=None,
                     help="profiling helper: run one leg only")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -304,8 +378,22 @@ def main():
         print(json.dumps({"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2}))
         return
 
+    if args.only == "prefill":
+        print(json.dumps(bench_prefill(torch, gk, dev, args.steps)))
+        return
+
     layers, caches, meta, scratch = build_config2(torch, gk, dev)
     step_bytes = sum(L.bytes for L in layers)
+    runner = StepRunner(torch, gk, dev, layers, caches, meta)
+    if args.only == "persistent":
+        for _ in range(args.steps):
+            runner(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert runner.status() == 0
+        sys.stdout.flush()
+        # Profiling helper only: skip interpreter teardown, where rocprofv3's
+        # tool has crashed after writing its output.
+        os._exit(0)
 
     def step(stream):
         for L in layers:
@@ -348,12 +436,18 @@ def main():
     s_gbs = s_bytes / (s_launch_us * 1e-6) / 1e9
     traffic = read_traffic("decode_split_global_ctx8192")
 
-    # ---- the headline: full 48-layer step, graph replay and eager
+    # ---- the headline: the whole step as one persistent launch, K launches
+    # back to back between events on the launch stream (so the time includes
+    # each launch's start-up), after W untimed ones.
     torch.cuda.synchronize()
-    ms_graph, _ = time_graph(torch, step, args.steps, args.warmup)
-    ms_eager = time_eager(torch, step, max(5, args.steps // 5), 2)
-    gbs = step_bytes / (ms_graph * 1e-3) / 1e9
-    gbs_eager = step_bytes / (ms_eager * 1e-3) / 1e9
+    ms_step = time_eager(torch, runner, args.steps, args.warmup)
+    status = runner.status()
+    if status != 0:
+        raise RuntimeError(f"decode step reported status {status}")
+    gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    # The per-layer-launch path for comparison (48 fused launches, graph replay).
+    ms_graph, _ = time_graph(torch, step, max(5, args.steps // 2), 2)
+    gbs_graph = step_bytes / (ms_graph * 1e-3) / 1e9
 
     result = {
         "metric": "decode attn+KV-append µs/layer-step and achieved HBM GB/s at batch 1 and 64",
@@ -362,8 +456,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_graph, 4),
-        "us_per_layer_step": round(ms_graph * 1e3 / NUM_LAYERS, 3),
+        "ms_per_step": round(ms_step, 4),
+        "us_per_layer_step": round(ms_step * 1e3 / NUM_LAYERS, 3),
         "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
         "higher_is_better": True,
         "scaling": "weak",
@@ -373,16 +467,23 @@ def main():
         "config": {"workload": "config2: 48 layers (40 sliding ring-1024 page-1 + 8 global page-64), "
                                "8 KV heads x 256, 16 q heads, batch 1, context 8192, fused append+decode",
                    "batch": 1, "context": CONTEXT, "layers": NUM_LAYERS,
-                   "bytes_per_step": step_bytes, "timing": "hipGraph replay of the 48 launches"},
-        "eager": {"ms_per_step": round(ms_eager, 4),
-                  "us_per_layer_step": round(ms_eager * 1e3 / NUM_LAYERS, 3),
-                  "achieved_GBs": round(gbs_eager, 1)},
-        "roofline": {"kernel": "decode_split_kernel<8x256>, global layer (8193 keys, fused append)",
-                     "bound": "hbm", "achieved": round(g_gbs, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(g_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": traffic, "avg_launch_us": round(g_launch_us, 3),
-                     "algorithmic_bytes_per_launch": g_bytes,
-                     "split_size": g_layers[0].split, "num_splits": g_layers[0].n_splits},
+                   "bytes_per_step": step_bytes,
+                   "timing": "one persistent launch per step (layer i waits for layer i-1's output)"},
+        "per_layer_launches": {"ms_per_step": round(ms_graph, 4),
+                               "us_per_layer_step": round(ms_graph * 1e3 / NUM_LAYERS, 3),
+                               "achieved_GBs": round(gbs_graph, 1),
+                               "timing": "hipGraph replay of 48 fused append+decode launches"},
+        "roofline": {"kernel": "decode_step_kernel (the whole 48-layer step, one launch)",
+                     "bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("decode_step_config2"),
+                     "avg_launch_us": round(ms_step * 1e3, 2),
+                     "algorithmic_bytes_per_launch": step_bytes},
+        "global_split_kernel": {"kernel": "decode_split_kernel<8x256>, global layer (8193 keys, fused append)",
+                                "avg_launch_us": round(g_launch_us, 3), "achieved_GBs": round(g_gbs, 1),
+                                "frac": round(g_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                                "algorithmic_bytes_per_launch": g_bytes,
+                                "split_size": g_layers[0].split, "num_splits": g_layers[0].n_splits},
         "sliding_split_kernel": {"avg_launch_us": round(s_launch_us, 3), "achieved_GBs": round(s_gbs, 1),
                                  "algorithmic_bytes_per_launch": s_bytes,
                                  "split_size": s_layers[0].split, "num_splits": s_layers[0].n_splits},
@@ -390,7 +491,9 @@ def main():
     if not args.no_batch64:
         b64 = bench_batch64(torch, gk, dev, max(3, args.steps // 5), 2)
         result["batch64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in b64.items()}
-    del caches
+    del caches, runner
+    if not args.no_prefill:
+        result["prefill_config5"] = bench_prefill(torch, gk, dev, max(5, args.steps // 2))
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result))

@@ -1,0 +1,833 @@
+// Persistent decode step for gfx950: one cooperative launch walks a run of
+// consecutive model layers, and for each layer appends the current token's
+// K/V and runs split-K GQA decode attention with its log-sum-exp combine.
+// Replaces the per-layer launches of the reference decode loop
+// (src/gemma4_decode_megakernel.cu:172-183 calling
+// gemma4_decode_megakernel_flash_attention_layer_bf16, whose append and
+// attention phases are src/gemma4_flash_attention_decode.cu:979-1067, with
+// grid.sync() between them).
+//
+// Layer order is a real data dependence: layer i's q and new K/V rows are
+// read only after every attention output row of layer i-1 has been
+// published, exactly as if layer i's projections consumed layer i-1's
+// output. What may run early is what does not depend on the previous layer:
+// the page-table lookups and the first K/V tiles of layer i (cache rows of
+// older tokens) are loaded into registers while layer i-1 is still being
+// combined, so the per-layer critical path is flag → q → math on resident
+// tiles → partial → combine → flag, and HBM streaming of the next layer
+// overlaps it.
+//
+// Decomposition (8 KV heads x 256 dims, 16 query heads, GQA group 2)
+//   One workgroup per CU (256), placed by the hardware round-robin over the
+//   8 XCDs. Each workgroup reads its XCD id and takes a ticket t (0..31)
+//   from that XCD's counter; the workgroups of XCD x serve KV head x of
+//   every sequence: sequence b = t % batch, split s = t / batch, with
+//   splits = 32 / batch per (sequence, head) "unit". All splits of a unit
+//   therefore share one L2, and their partials are exchanged through it.
+//   compute waves 0..3: 8-key tiles t = wave, wave+4, ... of the split
+//   control wave 4:     waits for the previous layer, then combines the
+//                       unit's splits for its own 8-dim slices of the output
+//                       rows (slices c = s, s + splits, ...) and signals
+// A tile is 8 keys x 256 dims of K and V: lane (r, c) loads the 16-byte pack
+// c of key rows 4r..4r+3 (rows 0-3 for lanes 0-31, 4-7 for lanes 32-63).
+//
+// Exchange between workgroups
+//   * split records (XCD-local): fp32 acc[2][256], (m, l)[2] per (layer
+//     parity, unit, split), written with ordinary stores (they reach the
+//     XCD's L2) and read with device-scope loads, which miss the L1 and are
+//     served from the L2 the writer shares. Empty dwords hold a
+//     signalling-NaN sentinel that arithmetic never produces, so readers
+//     poll the data itself. A writer empties its dwords one layer after
+//     they were combined; the parity continues across launches.
+//   * layer completion: each workgroup stores its output slices
+//     device-coherently, waits for them, then sets its XCD-local flag; the
+//     XCD's ticket-0 workgroup collects the 32 local flags and sets the XCD's
+//     device-coherent flag; every workgroup waits for all 8 XCD flags
+//     before reading the next layer's q. Flags hold the launch epoch
+//     (1 + the value the previous launch left in the workspace header), so
+//     they never need clearing.
+// The XCD mapping needs exactly 32 workgroups per XCD; workspace
+// initialisation checks that once by a probe launch of this kernel and
+// otherwise reports the entry point unsupported.
+// Every wait is bounded by the real-time clock: on expiry the launch sets an
+// error bit, stops waiting and drains (results are then undefined).
+#include "gemma4_device.hpp"
+#include "decode_common.hpp"
+
+#include "gemma4_flash_attention.h"
+
+#include <math.h>
+
+namespace gemma4 {
+namespace {
+
+// Model layer cadence (src/gemma4.h:105-108): every 6th layer and the last
+// one are global.
+constexpr int32_t kNumModelLayers = 48;
+constexpr int32_t kGlobalPeriod = 6;
+constexpr int kSHeads = 8, kSDim = 256, kSGroup = 2;
+constexpr int kComputeWaves = 4;
+constexpr int kStepThreads = (kComputeWaves + 1) * kWave;
+constexpr int kStepWorkgroups = 256;  // one workgroup per CU
+constexpr int kLPR = kSDim / kPackElems;      // 32 lanes per key row
+constexpr int kTileLoads = 4;                 // rows per lane per tile
+constexpr int kTileKeys = 2 * kTileLoads;     // 8 keys per tile
+constexpr int kNP = kTileLoads * kSGroup;     // partial dots per lane
+constexpr int kSBits = 2;                     // log2(kLPR / kNP)
+constexpr int kWaveKeys = 128;                // row-table entries per wave
+constexpr int kMaxSplitKeys = kComputeWaves * kWaveKeys;
+constexpr int kRowElems = kSHeads * kSDim;
+constexpr int kRecordFloats = 2 * kSDim + 8;  // acc[2][256], m0 l0 m1 l1, pad
+constexpr int kXcds = 8;                      // XCDs of an MI355X
+constexpr int kXcdSlots = 32;                 // workgroups (CUs) per XCD
+constexpr int kMaxBatch = 8;                  // at least 4 splits per unit
+constexpr uint32_t kSentinel = 0x7fa5a5a5u;   // signalling NaN
+constexpr int kHeaderInts = 64;               // epoch, error, record parity, pad
+constexpr int kHeaderEpoch = 0, kHeaderError = 1, kHeaderParity = 2;
+constexpr int kTicketStride = 32;             // ints between the XCD ticket counters
+constexpr int kGlobalFlagStride = 16;         // ints per layer: one flag per XCD
+constexpr size_t kPadLds = 96 * 1024;         // dynamic LDS that keeps one workgroup per CU
+constexpr uint64_t kWaitTicks = 100ull * 1000 * 1000 / 5;  // 0.2 s at 100 MHz
+constexpr int kPrefetchTiles = 4;             // register tile buffers per wave
+constexpr int kPolls = 3;                     // coherent polls in flight
+constexpr int kPollGap = 8;                   // s_sleep units (64 clocks) between them
+
+struct StepParams {
+  uint16_t *out;
+  const uint16_t *q;
+  const uint16_t *new_k;
+  const uint16_t *new_v;
+  uint16_t *cache_k[2];  // [0] sliding, [1] global
+  uint16_t *cache_v[2];
+  const int32_t *page_table[2];
+  Gemma4KvCacheConfig c[2];
+  const int32_t *seq_lengths;
+  const int32_t *token_position;
+  int32_t *header;
+  uint32_t *tickets;      // [xcd * kTicketStride]
+  int32_t *local_flags;   // [layer][xcd][slot]
+  int32_t *global_flags;  // [layer][kGlobalFlagStride]
+  float *records;
+  int32_t *probe;         // non-null: only report each workgroup's XCD id
+  int32_t batch;
+  int32_t first_layer;
+  int32_t layer_count;
+  int32_t units;
+  int32_t splits;
+  float q_scale;
+};
+
+__device__ __forceinline__ bool model_layer_global(int32_t layer) {
+  return layer == kNumModelLayers - 1 || (layer + 1) % kGlobalPeriod == 0;
+}
+// Index of `layer` among the cache layers of its own kind.
+__device__ __forceinline__ int32_t cache_layer_of(int32_t layer) {
+  const bool global = model_layer_global(layer);
+  int32_t index = 0;
+  for (int32_t l = 0; l < layer; ++l) index += model_layer_global(l) == global ? 1 : 0;
+  return index;
+}
+
+__device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
+
+// Id of the XCD (and so of the L2) this wave runs on.
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v;
+}
+// Reads of data another workgroup of the same XCD wrote with ordinary
+// stores. sc0|nt loads skip the CU's L1 (an sc0 load alone can still hit a
+// stale L1 line) and are served by the XCD's L2, clean or dirty, so a poll
+// costs an L2 round trip; device-scope (sc1) loads would go to memory for
+// every line the L2 holds clean.
+constexpr int kLocalLoadAux = 1 | 2;
+
+__device__ __forceinline__ int32_t coherent_load_i32(const int32_t *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void coherent_store_i32(int32_t *p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+using u32x2 = __attribute__((ext_vector_type(2))) unsigned;
+// Device-coherent buffer accesses at a per-lane byte offset from a
+// wave-uniform base (a per-lane base would force a loop over lanes).
+using BufferRsrc = decltype(__builtin_amdgcn_make_buffer_rsrc((void *)nullptr, 0, 0, 0));
+__device__ __forceinline__ BufferRsrc buffer_of(const void *base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0,
+                                           (int32_t)min<int64_t>(bytes, 0x7fffffff), 0x00020000);
+}
+// Ordinary store: written through the CU's L1 into the XCD's L2, where the
+// other workgroups of the XCD read it.
+__device__ __forceinline__ void local_store2(BufferRsrc r, int32_t off, float a, float b) {
+  const u32x2 v = {__float_as_uint(a), __float_as_uint(b)};
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
+}
+
+// Everything a compute wave needs about one layer of its split.
+struct LayerView {
+  const uint16_t *kbase;  // cache K at (head, lane pack), row 0
+  const uint16_t *vbase;
+  uint16_t *append_k;     // cache row of the appended token (head, lane pack) or null
+  uint16_t *append_v;
+  int32_t n_tiles;        // tiles of this wave
+  bool owner;             // this wave attends over the new token
+};
+
+__global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p) {
+  __shared__ int4 s_rows[kComputeWaves][kWaveKeys / 4];
+  __shared__ float s_prob[kComputeWaves][kWave];
+  __shared__ float s_ml[kComputeWaves][kSGroup][2];
+  __shared__ float s_acc[kComputeWaves][kSGroup][kSDim];
+
+  __shared__ int32_t s_ticket;
+
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = wave_uniform(threadIdx.x / kWave);
+  const int32_t xcd = (int32_t)(xcc_id() & 0xf);
+  if (p.probe != nullptr) {
+    if (threadIdx.x == 0) p.probe[blockIdx.x] = xcd;
+    return;
+  }
+  if (threadIdx.x == kComputeWaves * kWave) {
+    // Tickets count up forever; every launch takes exactly 32 per XCD.
+    s_ticket = (int32_t)(__hip_atomic_fetch_add(p.tickets + xcd * kTicketStride, 1u,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) %
+                         kXcdSlots);
+  }
+  __syncthreads();
+  const int32_t ticket = wave_uniform(s_ticket);
+  const bool active = ticket < p.batch * p.splits;
+  const int32_t b = active ? ticket % p.batch : 0;
+  const int32_t split = active ? ticket / p.batch : p.splits;  // inactive: no keys
+  const int32_t head = xcd;
+  const int32_t u = b * kSHeads + head;
+  const int32_t seq_len = wave_uniform(p.seq_lengths[b]);
+  const int32_t new_pos = wave_uniform(p.token_position[b]);
+  const int64_t q_stride = (int64_t)p.units * kSGroup * kSDim;  // per layer
+  const int64_t kv_stride = (int64_t)p.units * kSDim;
+  // Split records: one buffer over the whole region, addressed in bytes.
+  const BufferRsrc rec_buf =
+      buffer_of(p.records, 2ll * p.units * p.splits * kRecordFloats * 4);
+  // Record parity continues across launches (the header keeps it), so the
+  // record a layer writes was emptied one layer earlier, even for layer 0.
+  const int32_t epoch = coherent_load_i32(p.header + kHeaderEpoch) + 1;
+  const int32_t parity_base = coherent_load_i32(p.header + kHeaderParity);
+  auto record = [&](int32_t layer_i, int32_t s) -> int32_t {  // byte offset
+    return ((((parity_base + layer_i) & 1) * p.units + u) * p.splits + s) * (kRecordFloats * 4);
+  };
+
+  if (wave == kComputeWaves) {
+    // ------------------------------------------------------------ control
+    bool abort = false;
+    // A split longer than the row tables hold would drop keys: report it.
+    for (int kind = 0; kind < 2; ++kind) {
+      const Gemma4KvCacheConfig &c = p.c[kind];
+      int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;
+      first = first < 0 ? 0 : first;
+      const int32_t n_keys = seq_len > first ? seq_len - first : 0;
+      if ((n_keys + p.splits - 1) / p.splits > kMaxSplitKeys && lane == 0)
+        coherent_store_i32(p.header + kHeaderError, 2);
+    }
+    // Layer `layer_i` is complete once all 8 XCD flags read `epoch`.
+    auto wait_layer = [&](int32_t layer_i) {
+      const int32_t *row = p.global_flags + layer_i * kGlobalFlagStride;
+      const uint64_t t0 = now_ticks();
+      while (!abort) {
+        const bool ok = lane >= kXcds || coherent_load_i32(row + lane) == epoch;
+        if (__ballot(!ok) == 0) break;
+        if (now_ticks() - t0 > kWaitTicks) abort = true;
+      }
+    };
+    // Ticket 0 of each XCD: collect the XCD's 32 local flags, then raise
+    // the XCD's device-wide flag.
+    auto publish_xcd = [&](int32_t layer_i) {
+      const int32_t *row = p.local_flags + (layer_i * kXcds + xcd) * kXcdSlots;
+      const uint64_t t0 = now_ticks();
+      while (!abort) {
+        const bool ok = lane >= kXcdSlots ||
+                        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
+                            buffer_of(row, kXcdSlots * 4), lane * 4, 0, kLocalLoadAux) == epoch;
+        if (__ballot(!ok) == 0) break;
+        if (now_ticks() - t0 > kWaitTicks) abort = true;
+      }
+      if (lane == 0) coherent_store_i32(p.global_flags + layer_i * kGlobalFlagStride + xcd, epoch);
+    };
+    // Lane (sp, g) = (lane / 2, lane % 2) reads split sp's row g.
+    const int sp = lane >> 1;
+    const int g = lane & 1;
+    for (int32_t i = 0; i < p.layer_count; ++i) {
+      if (i > 0) wait_layer(i - 1);
+      __syncthreads();  // A: layer i may start
+      __syncthreads();  // B: this workgroup's compute waves finished layer i
+
+      // Combine unit u's splits for the 8-dim chunks c = split, split +
+      // splits, ... of both rows: one round of L2 loads per chunk.
+      for (int32_t c = split; active && c < kSDim / kPackElems; c += p.splits) {
+        // Lanes past the live splits read split 0 and weigh it zero.
+        const int32_t rec = record(i, sp < p.splits ? sp : 0);
+        const int32_t ml_off = rec + (2 * kSDim + 2 * g) * 4;
+        const int32_t acc_off = rec + (g * kSDim + c * kPackElems) * 4;
+        struct Poll {
+          u32x2 ml;
+          u32x4 lo, hi;
+        };
+        auto issue = [&](Poll &q) {
+          q.ml = __builtin_amdgcn_raw_buffer_load_b64(rec_buf, ml_off, 0, kLocalLoadAux);
+          q.lo = __builtin_amdgcn_raw_buffer_load_b128(rec_buf, acc_off, 0, kLocalLoadAux);
+          q.hi = __builtin_amdgcn_raw_buffer_load_b128(rec_buf, acc_off + 16, 0, kLocalLoadAux);
+        };
+        auto complete = [&](const Poll &q) {
+          bool bad = q.ml[0] == kSentinel || q.ml[1] == kSentinel;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bad |= q.lo[j] == kSentinel || q.hi[j] == kSentinel;
+          return __ballot(bad) == 0;
+        };
+        Poll polls[kPolls];
+#pragma unroll
+        for (int k = 0; k < kPolls; ++k) {
+          issue(polls[k]);
+          if (k + 1 < kPolls) __builtin_amdgcn_s_sleep(kPollGap);
+        }
+        // Wave-uniform index of the first complete poll. Each outcome gets
+        // its own copy of the reduction below, so only that poll's registers
+        // are read (the loads still in flight are never waited for).
+        int found = -1;
+        {
+          const uint64_t t0 = now_ticks();
+          while (found < 0 && !abort) {
+#pragma unroll
+            for (int k = 0; k < kPolls; ++k) {
+              if (found < 0) {
+                if (complete(polls[k])) {
+                  found = k;
+                } else {
+                  issue(polls[k]);
+                }
+              }
+            }
+            if (found < 0 && now_ticks() - t0 > kWaitTicks) abort = true;
+          }
+        }
+        auto finish = [&](const Poll &got) {
+        const bool live = sp < p.splits;
+        const float m_s = live ? __uint_as_float(got.ml[0]) : -INFINITY;
+        const float l_s = live ? __uint_as_float(got.ml[1]) : 0.0f;
+        // Reduce over the splits (lane bits 1..5) of each row g = lane bit 0.
+        float big_m = m_s;
+        big_m = fmaxf(big_m, lane_xor<2>(big_m));
+        big_m = fmaxf(big_m, lane_xor<4>(big_m));
+        big_m = fmaxf(big_m, lane_xor<8>(big_m));
+        big_m = fmaxf(big_m, lane_xor<16>(big_m));
+        big_m = fmaxf(big_m, lane_xor<32>(big_m));
+        const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
+        const float w = l_s > 0.0f ? __builtin_amdgcn_exp2f(m_s - m_ref) : 0.0f;
+        float big_l = w * l_s;
+        big_l += lane_xor<2>(big_l);
+        big_l += lane_xor<4>(big_l);
+        big_l += lane_xor<8>(big_l);
+        big_l += lane_xor<16>(big_l);
+        big_l += lane_xor<32>(big_l);
+        // Value-splitting sum of the 8 weighted dims: after the exchanges
+        // over lane bits 5, 4, 3 each lane holds the full sum of dim
+        // 4*b5 + 2*b4 + b3; bits 2 and 1 are then summed in place.
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[j] = w * __uint_as_float(got.lo[j]);
+          v[4 + j] = w * __uint_as_float(got.hi[j]);
+        }
+        {
+          const bool h = lane & 32;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float send = h ? v[j] : v[j + 4];
+            v[j] = (h ? v[j + 4] : v[j]) + lane_xor<32>(send);
+          }
+        }
+        {
+          const bool h = lane & 16;
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const float send = h ? v[j] : v[j + 2];
+            v[j] = (h ? v[j + 2] : v[j]) + lane_xor<16>(send);
+          }
+        }
+        {
+          const bool h = lane & 8;
+          const float send = h ? v[0] : v[1];
+          v[0] = (h ? v[1] : v[0]) + lane_xor<8>(send);
+        }
+        v[0] += lane_xor<4>(v[0]);
+        v[0] += lane_xor<2>(v[0]);
+        if ((lane & 6) == 0) {
+          const int dim = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+          const float inv = big_l > 0.0f ? 1.0f / big_l : 0.0f;
+          // Output rows go out device-coherent.
+          const BufferRsrc out_buf = buffer_of(p.out + i * q_stride, q_stride * 2);
+          __builtin_amdgcn_raw_buffer_store_b16(
+              (uint16_t)f32_to_bf16_bits(v[0] * inv), out_buf,
+              ((u * kSGroup + g) * kSDim + c * kPackElems + dim) * 2, 0, kCoherentAux);
+        }
+        };
+        static_assert(kPolls == 3, "one reduction copy per poll slot");
+        if (found == 1) {
+          finish(polls[1]);
+        } else if (found == 2) {
+          finish(polls[2]);
+        } else {
+          finish(polls[0]);
+        }
+      }
+      __syncthreads();  // C: records read; compute waves may prefetch
+      // My output slices are complete (device-wide) before my local flag.
+      wait_stores_complete();
+      if (lane == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(
+            (uint32_t)epoch, buffer_of(p.local_flags, (int64_t)kNumModelLayers * kXcds * kXcdSlots * 4),
+            ((i * kXcds + xcd) * kXcdSlots + ticket) * 4, 0, 0);
+      }
+      if (ticket == 0) publish_xcd(i);
+    }
+    if (xcd == 0 && ticket == 0) {
+      // Every workgroup has read the header (and finished): advance it.
+      wait_layer(p.layer_count - 1);
+      if (lane == 0) {
+        coherent_store_i32(p.header + kHeaderParity, (parity_base + p.layer_count) & 1);
+        coherent_store_i32(p.header + kHeaderEpoch, epoch);
+      }
+    }
+    if (abort && lane == 0) coherent_store_i32(p.header + kHeaderError, 1);
+    return;
+  }
+
+  // -------------------------------------------------------------- compute
+  const int r = lane / kLPR;      // row half of a load: key rows 4r..4r+3
+  const int cpack = lane % kLPR;  // 16-byte pack of the row
+  const int idx = cpack >> kSBits;
+  const int my_g = idx & (kSGroup - 1);
+  const int my_kl = idx / kSGroup;
+
+  // Layer view + row table for layer i of this split and wave: keys of the
+  // wave's tiles go to s_rows[wave] in tile order (tile i at 8i, key 4r+kl).
+  auto setup = [&](int32_t i) -> LayerView {
+    LayerView v;
+    const int32_t layer = p.first_layer + i;
+    const int kind = model_layer_global(layer) ? 1 : 0;
+    const Gemma4KvCacheConfig &c = p.c[kind];
+    const int32_t cache_layer = wave_uniform(cache_layer_of(layer));
+    int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;
+    first = first < 0 ? 0 : first;
+    const int32_t n_keys = seq_len > first ? seq_len - first : 0;
+    const int32_t split_size = (n_keys + p.splits - 1) / p.splits;
+    const int32_t k0 = first + split * split_size;
+    const int32_t k1 = active ? min(seq_len, k0 + split_size) : k0;
+    const int32_t tiles = k1 > k0 ? (k1 - k0 + kTileKeys - 1) / kTileKeys : 0;
+    v.n_tiles = tiles > wave ? min((tiles - wave + kComputeWaves - 1) / kComputeWaves,
+                                   kWaveKeys / kTileKeys)
+                             : 0;
+    const bool live_new = new_pos >= first && new_pos < seq_len;
+    const int32_t owner_split = live_new ? (new_pos - first) / max(split_size, 1) : 0;
+    const int32_t owner_wave = live_new ? ((new_pos - k0) / kTileKeys) % kComputeWaves : 0;
+    const int32_t new_row = split == owner_split && wave == owner_wave
+                                ? append_row(c, p.page_table[kind], cache_layer, b, new_pos)
+                                : -1;
+    v.owner = live_new && split == owner_split && wave == owner_wave;
+    const int64_t col = (int64_t)head * kSDim + cpack * kPackElems;
+    v.kbase = p.cache_k[kind] + col;
+    v.vbase = p.cache_v[kind] + col;
+    v.append_k = new_row >= 0 ? p.cache_k[kind] + (int64_t)new_row * kRowElems + col : nullptr;
+    v.append_v = new_row >= 0 ? p.cache_v[kind] + (int64_t)new_row * kRowElems + col : nullptr;
+    // Two table entries per lane: wave-local key e = lane, lane + 64.
+    const int32_t *pt = p.page_table[kind] + b * c.max_pages_per_seq;
+    int32_t rows[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int e = lane + h * kWave;
+      const int32_t t = wave + (e / kTileKeys) * kComputeWaves;
+      const int32_t key = k0 + t * kTileKeys + e % kTileKeys;
+      const int32_t logical = key / c.page_size;
+      const int32_t physical = pt[logical % c.max_pages_per_seq];
+      const bool ok = e / kTileKeys < v.n_tiles && key < k1 && !(live_new && key == new_pos) &&
+                      physical >= 0 && physical < c.num_pages;
+      rows[h] = ok ? ((cache_layer * c.num_pages + physical) * c.page_size +
+                      (key - logical * c.page_size))
+                   : kRowInvalid;
+    }
+    int32_t *tab = reinterpret_cast<int32_t *>(s_rows[wave]);
+    tab[lane] = rows[0];
+    tab[lane + kWave] = rows[1];
+    wave_lds_sync();
+    return v;
+  };
+
+  struct TileBuf {
+    uint4 k[kTileLoads], v[kTileLoads];
+    uint32_t valid;
+  };
+  auto issue = [&](TileBuf &tb, const LayerView &v, int t) {
+    const int4 rr = s_rows[wave][t * 2 + r];
+    const int32_t rows[4] = {rr.x, rr.y, rr.z, rr.w};
+    tb.valid = 0;
+#pragma unroll
+    for (int kl = 0; kl < kTileLoads; ++kl) {
+      tb.valid |= (rows[kl] >= 0 ? 1u : 0u) << kl;
+      const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems;
+      tb.k[kl] = load128(v.kbase + off);
+      tb.v[kl] = load128(v.vbase + off);
+    }
+  };
+
+  uint32_t qw[kSGroup][4];
+  float m[kSGroup], acc[kSGroup][8], l_lane;
+  auto compute = [&](const TileBuf &t) {
+    float part[kNP];
+#pragma unroll
+    for (int kl = 0; kl < kTileLoads; ++kl) {
+      const uint32_t kw[4] = {t.k[kl].x, t.k[kl].y, t.k[kl].z, t.k[kl].w};
+#pragma unroll
+      for (int g = 0; g < kSGroup; ++g) {
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a = dot2_bf16(qw[g][j], kw[j], a);
+        part[kl * kSGroup + g] = a;
+      }
+    }
+    split_butterfly<kNP, kLPR / 2>(part, lane);
+    const bool valid = (t.valid >> my_kl) & 1u;
+    const float score = valid ? part[0] * p.q_scale : -INFINITY;
+    float tmax[kSGroup];
+    gather_heads<kSGroup, kSBits>(reduce_max_from<(1 << kSBits) * kSGroup>(score), my_g, tmax);
+    float alpha[kSGroup], m_use[kSGroup];
+#pragma unroll
+    for (int g = 0; g < kSGroup; ++g) {
+      const float m_new = fmaxf(m[g], tmax[g]);
+      m_use[g] = m_new == -INFINITY ? 0.0f : m_new;
+      alpha[g] = __builtin_amdgcn_exp2f(m[g] - m_use[g]);
+      m[g] = m_new;
+    }
+    const float my_m = my_g ? m_use[1] : m_use[0];
+    const float my_alpha = my_g ? alpha[1] : alpha[0];
+    const float prob = __builtin_amdgcn_exp2f(score - my_m);
+    l_lane = l_lane * my_alpha + prob;
+    s_prob[wave][r * kNP + idx] = prob;
+    wave_lds_sync();
+    float pv[kNP];
+#pragma unroll
+    for (int i = 0; i < kNP; i += 4) {
+      const float4 q4 = *reinterpret_cast<const float4 *>(&s_prob[wave][r * kNP + i]);
+      pv[i] = q4.x; pv[i + 1] = q4.y; pv[i + 2] = q4.z; pv[i + 3] = q4.w;
+    }
+#pragma unroll
+    for (int g = 0; g < kSGroup; ++g) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] *= alpha[g];
+    }
+#pragma unroll
+    for (int kl = 0; kl < kTileLoads; ++kl) {
+      float vf[8];
+      const uint4 vp = (t.valid >> kl) & 1u ? t.v[kl] : make_uint4(0, 0, 0, 0);
+      unpack8(vp, vf);
+#pragma unroll
+      for (int g = 0; g < kSGroup; ++g) {
+        const float w = pv[kl * kSGroup + g];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(w, vf[j], acc[g][j]);
+      }
+    }
+  };
+
+  TileBuf buf[kPrefetchTiles];
+  LayerView view = setup(0);
+#pragma unroll
+  for (int j = 0; j < kPrefetchTiles; ++j)
+    if (j < view.n_tiles) issue(buf[j], view, j);
+
+  // This wave's record dwords: head g = lane / 32, dims d, d+1 of its quarter.
+  const int rec_g = lane / kLPR;
+  const int rec_d = wave * (kSDim / kComputeWaves) + (lane % kLPR) * 2;
+
+  for (int32_t i = 0; i < p.layer_count; ++i) {
+    __syncthreads();  // A: layer i-1 published (or i == 0)
+    if (active) {
+      // Layer i-1's record (for i == 0 the previous launch's last one) has
+      // been combined by every reader: reset my dwords to empty.
+      const int32_t rec = record(i - 1, split);
+      const float sf = __uint_as_float(kSentinel);
+      local_store2(rec_buf, rec + (rec_g * kSDim + rec_d) * 4, sf, sf);
+      if (wave == 0 && (lane & (kLPR - 1)) == 0)
+        local_store2(rec_buf, rec + (2 * kSDim + 2 * rec_g) * 4, sf, sf);
+    }
+    // q rows of the two query heads of this kv head, packed bf16.
+    const uint16_t *qrow = p.q + i * q_stride + (int64_t)u * kSGroup * kSDim + cpack * kPackElems;
+#pragma unroll
+    for (int g = 0; g < kSGroup; ++g) {
+      const uint4 qp = load128(qrow + g * kSDim);
+      qw[g][0] = qp.x; qw[g][1] = qp.y; qw[g][2] = qp.z; qw[g][3] = qp.w;
+      m[g] = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+    }
+    l_lane = 0.0f;
+    uint4 nk = make_uint4(0, 0, 0, 0), nv = nk;
+    const bool appender = view.append_k != nullptr;
+    if (view.owner || appender) {
+      const int64_t src = i * kv_stride + (int64_t)u * kSDim + cpack * kPackElems;
+      nk = load128(p.new_k + src);
+      nv = load128(p.new_v + src);
+    }
+
+    for (int32_t t0 = 0; t0 < view.n_tiles; t0 += kPrefetchTiles) {
+#pragma unroll
+      for (int j = 0; j < kPrefetchTiles; ++j) {
+        if (t0 + j < view.n_tiles) compute(buf[j]);
+        if (t0 + j + kPrefetchTiles < view.n_tiles) issue(buf[j], view, t0 + j + kPrefetchTiles);
+      }
+    }
+    if (view.owner) {
+      // The appended token: row 0 of a one-key tile, read from new K/V.
+      TileBuf nt;
+#pragma unroll
+      for (int kl = 0; kl < kTileLoads; ++kl) { nt.k[kl] = nk; nt.v[kl] = nv; }
+      nt.valid = r == 0 ? 1u : 0u;
+      compute(nt);
+    }
+    if (appender && r == 0) {
+      store128(view.append_k, nk);
+      store128(view.append_v, nv);
+    }
+
+    // Wave totals to LDS, then the four waves' partials are merged.
+    float l_head[kSGroup];
+    gather_heads<kSGroup, kSBits>(reduce_sum_from<(1 << kSBits) * kSGroup>(l_lane), my_g, l_head);
+#pragma unroll
+    for (int g = 0; g < kSGroup; ++g) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[g][j] = sum_rows<kLPR>(acc[g][j]);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int g = 0; g < kSGroup; ++g) {
+        s_ml[wave][g][0] = m[g];
+        s_ml[wave][g][1] = l_head[g];
+      }
+    }
+    if (r == 0) {
+#pragma unroll
+      for (int g = 0; g < kSGroup; ++g) {
+        float4 *dst = reinterpret_cast<float4 *>(&s_acc[wave][g][cpack * 8]);
+        dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
+      }
+    }
+    __syncthreads();  // B
+    {
+      float big_m = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kComputeWaves; ++w) big_m = fmaxf(big_m, s_ml[w][rec_g][0]);
+      const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
+      float big_l = 0.0f, a0 = 0.0f, a1 = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kComputeWaves; ++w) {
+        const float f = __builtin_amdgcn_exp2f(s_ml[w][rec_g][0] - m_ref);
+        big_l = fmaf(s_ml[w][rec_g][1], f, big_l);
+        const float2 a = *reinterpret_cast<const float2 *>(&s_acc[w][rec_g][rec_d]);
+        a0 = fmaf(a.x, f, a0);
+        a1 = fmaf(a.y, f, a1);
+      }
+      // My reset of these dwords (one layer ago) must land before the data.
+      wait_stores_complete();
+      if (active) {
+        const int32_t rec = record(i, split);
+        local_store2(rec_buf, rec + (rec_g * kSDim + rec_d) * 4, a0, a1);
+        if (wave == 0 && (lane & (kLPR - 1)) == 0)
+          local_store2(rec_buf, rec + (2 * kSDim + 2 * rec_g) * 4, big_m, big_l);
+      }
+    }
+    // C: the control wave has read the split records. The next layer's
+    // tiles are issued only now, so their HBM traffic does not queue ahead
+    // of the record reads on this layer's critical path.
+    __syncthreads();
+    if (i + 1 < p.layer_count) {
+      view = setup(i + 1);
+#pragma unroll
+      for (int j = 0; j < kPrefetchTiles; ++j)
+        if (j < view.n_tiles) issue(buf[j], view, j);
+    }
+  }
+}
+
+__global__ void decode_step_workspace_init_kernel(int32_t *ints, int64_t n_ints,
+                                                  uint32_t *records, int64_t n_records) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n_ints; x += stride)
+    ints[x] = 0;
+  for (int64_t x = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; x < n_records; x += stride)
+    records[x] = kSentinel;
+}
+
+// Workspace: header | XCD ticket counters | local flags | global flags |
+// probe slots | split records (sentinel-filled).
+struct WorkspaceLayout {
+  int32_t units, splits;
+  int64_t tickets, local_flags, global_flags, probe, int_count, record_floats, bytes;
+};
+WorkspaceLayout workspace_layout(int32_t batch_count) {
+  WorkspaceLayout w{};
+  w.units = batch_count * kSHeads;
+  w.splits = batch_count > 0 ? kXcdSlots / batch_count : 0;
+  w.tickets = kHeaderInts;
+  w.local_flags = w.tickets + kXcds * kTicketStride;
+  w.global_flags = w.local_flags + (int64_t)kNumModelLayers * kXcds * kXcdSlots;
+  w.probe = w.global_flags + (int64_t)kNumModelLayers * kGlobalFlagStride;
+  w.int_count = w.probe + kStepWorkgroups;
+  w.record_floats = 2ll * w.units * w.splits * kRecordFloats;
+  w.bytes = (w.int_count + w.record_floats) * 4;
+  return w;
+}
+
+// Per-device result of the placement probe: 0 unknown, 1 ok, -1 unsupported.
+int g_placement_ok[64];
+
+StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_count) {
+  StepParams p{};
+  int32_t *ints = static_cast<int32_t *>(workspace);
+  p.header = ints;
+  p.tickets = reinterpret_cast<uint32_t *>(ints + w.tickets);
+  p.local_flags = ints + w.local_flags;
+  p.global_flags = ints + w.global_flags;
+  p.records = reinterpret_cast<float *>(ints + w.int_count);
+  p.batch = batch_count;
+  p.units = w.units;
+  p.splits = w.splits;
+  return p;
+}
+
+hipError_t launch_step(StepParams &p, hipStream_t stream) {
+  void *args[] = {&p};
+  return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(decode_step_kernel),
+                                    dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds,
+                                    stream);
+}
+
+bool step_geometry_ok(const Gemma4KvCacheConfig &c, int32_t batch_count) {
+  return c.num_heads == kSHeads && c.head_dim == kSDim && c.page_size > 0 &&
+         c.max_pages_per_seq > 0 && c.num_pages > 0 && c.batch_size >= batch_count;
+}
+
+}  // namespace
+}  // namespace gemma4
+
+using namespace gemma4;
+
+extern "C" size_t gemma4_decode_step_workspace_bytes(int32_t batch_count) {
+  if (batch_count < 1 || batch_count > kMaxBatch) return 0;
+  return (size_t)workspace_layout(batch_count).bytes;
+}
+
+extern "C" hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t workspace_bytes,
+                                                        int32_t batch_count, hipStream_t stream) {
+  const size_t need = gemma4_decode_step_workspace_bytes(batch_count);
+  if (workspace == nullptr || need == 0 || workspace_bytes < need) return hipErrorInvalidValue;
+  const WorkspaceLayout w = workspace_layout(batch_count);
+  int32_t *ints = static_cast<int32_t *>(workspace);
+  hipLaunchKernelGGL(decode_step_workspace_init_kernel, 256, 256, 0, stream, ints, w.int_count,
+                     reinterpret_cast<uint32_t *>(ints + w.int_count), w.record_floats);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  int device = 0;
+  e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  if (device < 0 || device >= 64) return hipErrorNotSupported;
+  if (g_placement_ok[device] == 0) {
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_step_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPadLds);
+    if (e != hipSuccess) return e;
+    // One probe launch of the step kernel: every XCD must receive exactly
+    // 32 of its workgroups (one per CU) for the XCD-local exchange.
+    StepParams p = base_params(workspace, w, batch_count);
+    p.probe = ints + w.probe;
+    e = launch_step(p, stream);
+    if (e != hipSuccess) return e;
+    int32_t ids[kStepWorkgroups];
+    e = hipMemcpyAsync(ids, p.probe, sizeof(ids), hipMemcpyDeviceToHost, stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return e;
+    int count[16] = {};
+    bool ok = true;
+    for (int32_t id : ids) {
+      if (id < 0 || id >= kXcds) ok = false;
+      else ++count[id];
+    }
+    for (int x = 0; x < kXcds; ++x) ok &= count[x] == kXcdSlots;
+    g_placement_ok[device] = ok ? 1 : -1;
+  }
+  return g_placement_ok[device] == 1 ? hipSuccess : hipErrorNotSupported;
+}
+
+extern "C" hipError_t gemma4_decode_step_status(const void *workspace, int32_t *status) {
+  if (workspace == nullptr || status == nullptr) return hipErrorInvalidValue;
+  int32_t header[2] = {0, 0};
+  const hipError_t e = hipMemcpy(header, workspace, sizeof(header), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return e;
+  *status = header[1];
+  return hipSuccess;
+}
+
+extern "C" hipError_t gemma4_decode_step_layers_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
+    const int32_t *sliding_page_table, Gemma4KvCacheConfig sliding_config,
+    gemma4_bf16 *global_cache_k, gemma4_bf16 *global_cache_v,
+    const int32_t *global_page_table, Gemma4KvCacheConfig global_config,
+    const int32_t *seq_lengths, const int32_t *token_position, int32_t first_layer,
+    int32_t layer_count, float scale, int32_t batch_count, void *workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+  const size_t need = gemma4_decode_step_workspace_bytes(batch_count);
+  if (out == nullptr || q == nullptr || k == nullptr || v == nullptr || seq_lengths == nullptr ||
+      token_position == nullptr || workspace == nullptr || need == 0 || workspace_bytes < need ||
+      first_layer < 0 || layer_count < 1 || first_layer + layer_count > kNumModelLayers ||
+      !(scale > 0.0f))
+    return hipErrorInvalidValue;
+  const WorkspaceLayout w = workspace_layout(batch_count);
+  bool need_kind[2] = {false, false};
+  for (int32_t l = first_layer; l < first_layer + layer_count; ++l)
+    need_kind[(l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0) ? 1 : 0] = true;
+  const Gemma4KvCacheConfig cfg[2] = {sliding_config, global_config};
+  gemma4_bf16 *ck[2] = {sliding_cache_k, global_cache_k};
+  gemma4_bf16 *cv[2] = {sliding_cache_v, global_cache_v};
+  const int32_t *pt[2] = {sliding_page_table, global_page_table};
+  for (int kind = 0; kind < 2; ++kind) {
+    if (!need_kind[kind]) continue;
+    const Gemma4KvCacheConfig &c = cfg[kind];
+    if (ck[kind] == nullptr || cv[kind] == nullptr || pt[kind] == nullptr ||
+        !step_geometry_ok(c, batch_count) || (kind == 0) != (c.window_size > 0))
+      return hipErrorInvalidValue;
+    // Longest live key range a sequence can have in this cache, per split.
+    const int64_t live = kind == 0 ? c.window_size : (int64_t)c.max_pages_per_seq * c.page_size;
+    if ((live + w.splits - 1) / w.splits > kMaxSplitKeys) return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)c.num_layers * c.num_pages * c.page_size;
+    if (rows * kRowElems >= (int64_t)1 << 31 || c.num_layers < 1) return hipErrorInvalidValue;
+  }
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64 ||
+      g_placement_ok[device] != 1)
+    return hipErrorNotSupported;  // gemma4_decode_step_workspace_init first
+  StepParams p = base_params(workspace, w, batch_count);
+  p.out = reinterpret_cast<uint16_t *>(out);
+  p.q = reinterpret_cast<const uint16_t *>(q);
+  p.new_k = reinterpret_cast<const uint16_t *>(k);
+  p.new_v = reinterpret_cast<const uint16_t *>(v);
+  for (int kind = 0; kind < 2; ++kind) {
+    p.cache_k[kind] = reinterpret_cast<uint16_t *>(ck[kind]);
+    p.cache_v[kind] = reinterpret_cast<uint16_t *>(cv[kind]);
+    p.page_table[kind] = pt[kind];
+    p.c[kind] = cfg[kind];
+  }
+  p.seq_lengths = seq_lengths;
+  p.token_position = token_position;
+  p.first_layer = first_layer;
+  p.layer_count = layer_count;
+  p.q_scale = scale * kLog2e;
+  return launch_step(p, stream);
+}

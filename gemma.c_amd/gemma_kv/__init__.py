@@ -91,6 +91,12 @@ SIGNATURES = {
     "gemma4_runtime_set_host_seq_lengths": (_I32, [_P, _P, _I64]),
     "gemma4_runtime_device_ptr": (_P, [_P, _I32]),
     "gemma4_decode_split_plan": (_I32, [_CFG, _I32, _I32, _I32, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
+    "gemma4_decode_step_workspace_bytes": (ctypes.c_size_t, [_I32]),
+    "gemma4_decode_step_workspace_init": (_I32, [_P, ctypes.c_size_t, _I32, _P]),
+    "gemma4_decode_step_status": (_I32, [_P, ctypes.POINTER(_I32)]),
+    "gemma4_decode_step_layers_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _CFG, _P, _P, _P, _CFG, _P, _P, _I32, _I32, _F32,
+               _I32, _P, ctypes.c_size_t, _P]),
 }
 
 _lib: Optional[ctypes.CDLL] = None
@@ -241,6 +247,36 @@ def flash_attention_decode_combine_bf16(out, partial_m, partial_l, partial_acc,
     return lib().gemma4_flash_attention_decode_combine_bf16(
         ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(seq_lengths),
         config, split_size, num_splits, batch_count, stream_handle(stream))
+
+
+def decode_step_workspace_bytes(batch_count: int) -> int:
+    return lib().gemma4_decode_step_workspace_bytes(batch_count)
+
+
+def decode_step_workspace_init(workspace, batch_count: int, stream=None) -> int:
+    return lib().gemma4_decode_step_workspace_init(
+        ptr(workspace), workspace.numel() * workspace.element_size(), batch_count,
+        stream_handle(stream))
+
+
+def decode_step_status(workspace) -> int:
+    st = _I32()
+    check(lib().gemma4_decode_step_status(ptr(workspace), ctypes.byref(st)),
+          "gemma4_decode_step_status")
+    return st.value
+
+
+def decode_step_layers_bf16(out, q, k, v, sliding_k, sliding_v, sliding_page_table,
+                            sliding_config, global_k, global_v, global_page_table,
+                            global_config, seq_lengths, token_position, first_layer,
+                            layer_count, softmax_scale, batch_count, workspace,
+                            stream=None) -> int:
+    return lib().gemma4_decode_step_layers_bf16(
+        ptr(out), ptr(q), ptr(k), ptr(v), ptr(sliding_k), ptr(sliding_v),
+        ptr(sliding_page_table), sliding_config, ptr(global_k), ptr(global_v),
+        ptr(global_page_table), global_config, ptr(seq_lengths), ptr(token_position),
+        first_layer, layer_count, softmax_scale, batch_count, ptr(workspace),
+        workspace.numel() * workspace.element_size(), stream_handle(stream))
 
 
 class Runtime:

@@ -123,6 +123,42 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
                                     int32_t target_workgroups,
                                     int32_t *split_size, int32_t *num_splits);
 
+// ---- persistent decode step over consecutive layers --------------------
+// One cooperative launch that runs, for model layers first_layer ..
+// first_layer + layer_count - 1 in order, the fused K/V append of the current
+// token and the split-K decode attention with its combine, for `batch_count`
+// sequences. Replaces the per-layer attention launches of the reference
+// decode loop (src/gemma4_decode_megakernel.cu:172-183 ->
+// gemma4_decode_megakernel_flash_attention_layer_bf16, append + attention
+// phases src/gemma4_flash_attention_decode.cu:979-1067).
+//   q, out: [layer_count][batch_count][16][256] bf16; k, v (the appended
+//   rows): [layer_count][batch_count][8][256]. Layer i reads q/k/v[i] only
+//   after out[i-1] is complete (the order a real decode step imposes).
+//   Sliding layers use the sliding cache/config/page table, global layers
+//   (every 6th and the last) the global ones; both geometries must be 8 KV
+//   heads x 256. seq_lengths / token_position: as for the per-layer entry
+//   points (one step: the same for every layer).
+// `workspace` (gemma4_decode_step_workspace_bytes bytes) holds the split
+// records and layer flags; initialise it once with
+// gemma4_decode_step_workspace_init, then reuse it for every step (stream
+// order). Calls sharing a workspace must not overlap. After a call,
+// gemma4_decode_step_status reports 0, or a nonzero code if a bounded wait
+// expired (1; the workspace must then be initialised again) or a split
+// exceeded the 512-key table (2).
+size_t gemma4_decode_step_workspace_bytes(int32_t batch_count);
+hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t workspace_bytes,
+                                             int32_t batch_count, hipStream_t stream);
+hipError_t gemma4_decode_step_status(const void *workspace, int32_t *status);
+hipError_t gemma4_decode_step_layers_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
+    const int32_t *sliding_page_table, Gemma4KvCacheConfig sliding_config,
+    gemma4_bf16 *global_cache_k, gemma4_bf16 *global_cache_v,
+    const int32_t *global_page_table, Gemma4KvCacheConfig global_config,
+    const int32_t *seq_lengths, const int32_t *token_position, int32_t first_layer,
+    int32_t layer_count, float scale, int32_t batch_count, void *workspace,
+    size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }  // extern "C"
 #endif

@@ -1,0 +1,216 @@
+"""Parity of the persistent multi-layer decode step
+(gemma4_decode_step_layers_bf16) against the CPU oracle applied layer by
+layer (append, then attend), and at the full BASELINE config-2 size against
+the per-layer fused append+decode entry point. Appends are bit-exact;
+attention outputs within max_abs 2e-2 / max_rel 1e-2."""
+import math
+
+import numpy as np
+import pytest
+
+import gemma_kv as gk
+from kvtest import (assert_close, cache_config, empty_bf16, fill_page_table,
+                    from_dev_bf16, randn_bf16, ring_pages, to_dev)
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+HEADS, DIM = 8, 256
+
+
+def is_global(layer):
+    return layer == 47 or (layer + 1) % 6 == 0
+
+
+def _workspace(dev, batch):
+    import torch
+    nbytes = gk.decode_step_workspace_bytes(batch)
+    assert nbytes > 0
+    ws = torch.empty(nbytes // 4, dtype=torch.int32, device=dev)
+    gk.check(gk.decode_step_workspace_init(ws, batch), "workspace_init")
+    return ws
+
+
+def _case(rng, first_layer, layer_count, seq, window, s_page, g_page):
+    batch = len(seq)
+    layers = list(range(first_layer, first_layer + layer_count))
+    n_s = sum(1 for l in range(48) if not is_global(l))
+    n_g = 48 - n_s
+    s_max = ring_pages(window, s_page)
+    g_max = (max(seq) + g_page - 1) // g_page
+    s_cfg = cache_config(n_s, batch, s_page, s_max, HEADS, DIM, window)
+    g_cfg = cache_config(n_g, batch, g_page, g_max, HEADS, DIM, 0)
+    s_pt = fill_page_table(s_cfg, seq)
+    g_pt = fill_page_table(g_cfg, seq)
+    caches = {
+        "sk": randn_bf16(rng, (s_cfg[0] * s_cfg[1] * s_page, HEADS, DIM)),
+        "sv": randn_bf16(rng, (s_cfg[0] * s_cfg[1] * s_page, HEADS, DIM)),
+        "gk": randn_bf16(rng, (g_cfg[0] * g_cfg[1] * g_page, HEADS, DIM)),
+        "gv": randn_bf16(rng, (g_cfg[0] * g_cfg[1] * g_page, HEADS, DIM)),
+    }
+    q = randn_bf16(rng, (layer_count, batch, 16, DIM))
+    k = randn_bf16(rng, (layer_count, batch, HEADS, DIM))
+    v = randn_bf16(rng, (layer_count, batch, HEADS, DIM))
+    return layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v
+
+
+def _expected(layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v, seq, pos, scale):
+    exp = {n: a.copy() for n, a in caches.items()}
+    outs = []
+    batch = len(seq)
+    for i, layer in enumerate(layers):
+        g = is_global(layer)
+        cfg, pt = (g_cfg, g_pt) if g else (s_cfg, s_pt)
+        ck, cv = (exp["gk"], exp["gv"]) if g else (exp["sk"], exp["sv"])
+        cl = oracle.layer_index(layer, g)
+        oracle.kv_cache_write(ck, cv, cfg, pt, list(range(batch)), pos, cl, k[i], v[i])
+        outs.append(oracle.decode_attention(q[i], ck, cv, pt, seq, cfg, cl, scale))
+    return exp, np.stack(outs)
+
+
+def _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos, scale):
+    import torch
+    batch = len(seq)
+    out = empty_bf16((len(layers), batch, 16, DIM), dev)
+    code = gk.decode_step_layers_bf16(
+        out, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), dcaches["sk"], dcaches["sv"],
+        to_dev(s_pt, dev), gk.make_config(*s_cfg), dcaches["gk"], dcaches["gv"],
+        to_dev(g_pt, dev), gk.make_config(*g_cfg), to_dev(np.asarray(seq, np.int32), dev),
+        to_dev(np.asarray(pos, np.int32), dev), layers[0], len(layers), scale, batch, ws)
+    gk.check(code, "decode_step")
+    torch.cuda.synchronize()
+    assert gk.decode_step_status(ws) == 0
+    return from_dev_bf16(out)
+
+
+STEP_CASES = [
+    # first_layer, layer_count, seq_lengths, window, sliding page, global page
+    (0, 7, [151], 64, 1, 16),          # ring wrapped, 5 sliding + global + sliding
+    (3, 4, [40], 64, 4, 16),           # window not yet full, page-4 ring
+    (0, 12, [9], 1024, 1, 64),         # fewer keys than splits: empty splits
+    (44, 4, [300, 77], 128, 1, 64),    # batch 2, ends at the last (global) layer
+    (5, 1, [1], 1024, 1, 64),          # one global layer, first token
+    (0, 6, [2000, 1, 513], 256, 16, 64),  # batch 3 (10 splits per unit), ragged
+]
+
+
+@pytest.mark.parametrize("first,count,seq,window,s_page,g_page", STEP_CASES)
+def test_decode_step_against_oracle(dev, first, count, seq, window, s_page, g_page):
+    rng = np.random.default_rng(sum(seq) + first * 7 + count)
+    layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v = _case(
+        rng, first, count, seq, window, s_page, g_page)
+    pos = [n - 1 for n in seq]
+    scale = 1 / math.sqrt(DIM)
+    exp_caches, exp_out = _expected(layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v, seq,
+                                    pos, scale)
+    dcaches = {n: to_dev(a, dev) for n, a in caches.items()}
+    ws = _workspace(dev, len(seq))
+    got = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos,
+                    scale)
+    for n in caches:
+        assert np.array_equal(from_dev_bf16(dcaches[n]).reshape(caches[n].shape),
+                              exp_caches[n]), n
+    for i, layer in enumerate(layers):
+        assert_close(got[i], exp_out[i], f"layer {layer}")
+    # Same workspace again (next epoch): the appended rows are already in
+    # place, so the same step gives the same outputs.
+    again = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos,
+                      scale)
+    assert np.array_equal(again, got)
+
+
+def test_decode_step_rejects_bad_arguments(dev):
+    import torch
+    rng = np.random.default_rng(1)
+    layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v = _case(rng, 0, 2, [10], 64, 1, 16)
+    ws = _workspace(dev, 1)
+    out = empty_bf16((2, 1, 16, DIM), dev)
+    d = {n: to_dev(a, dev) for n, a in caches.items()}
+    seq = to_dev(np.asarray([10], np.int32), dev)
+    pos = to_dev(np.asarray([9], np.int32), dev)
+    args = [out, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), d["sk"], d["sv"],
+            to_dev(s_pt, dev), gk.make_config(*s_cfg), d["gk"], d["gv"], to_dev(g_pt, dev),
+            gk.make_config(*g_cfg), seq, pos]
+    bad_geom = gk.make_config(*cache_config(40, 1, 1, 64, 1, 512, 64))
+    assert gk.decode_step_layers_bf16(*args, 47, 2, 0.0625, 1, ws) != 0   # past layer 47
+    assert gk.decode_step_layers_bf16(*args, 0, 2, 0.0, 1, ws) != 0       # scale
+    assert gk.decode_step_layers_bf16(*args, 0, 2, 0.0625, 9, ws) != 0    # batch > 8
+    bad = list(args)
+    bad[7] = bad_geom
+    assert gk.decode_step_layers_bf16(*bad, 0, 2, 0.0625, 1, ws) != 0     # 1x512
+    small = torch.empty(16, dtype=torch.int32, device=dev)
+    assert gk.decode_step_layers_bf16(*args, 0, 2, 0.0625, 1, small) != 0  # workspace
+    torch.cuda.synchronize()
+
+
+def test_decode_step_config2_matches_per_layer_path(dev):
+    """BASELINE config 2 at full size (48 layers, context 8192, sliding page 1,
+    global page 64): the persistent step against 48 per-layer fused
+    append+decode launches on a copy of the same caches."""
+    import torch
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    seq_len, pos = 8193, 8192
+    n_s, n_g = 40, 8
+    s_cfg = cache_config(n_s, 1, 1, 1024, HEADS, DIM, 1024)
+    g_pages = (seq_len + 63) // 64
+    g_cfg = cache_config(n_g, 1, 64, g_pages, HEADS, DIM, 0)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=gen, device=dev).bfloat16().view(torch.int16)
+
+    caches = {"sk": rnd((n_s * 1024, HEADS, DIM)), "sv": rnd((n_s * 1024, HEADS, DIM)),
+              "gk": rnd((n_g * g_pages * 64, HEADS, DIM)),
+              "gv": rnd((n_g * g_pages * 64, HEADS, DIM))}
+    ref_caches = {n: t.clone() for n, t in caches.items()}
+    q, k, v = rnd((48, 1, 16, DIM)), rnd((48, 1, HEADS, DIM)), rnd((48, 1, HEADS, DIM))
+    i32 = dict(dtype=torch.int32, device=dev)
+    s_pt = torch.arange(1024, **i32)
+    g_pt = torch.arange(g_pages, **i32)
+    seq_t = torch.tensor([seq_len], **i32)
+    pos_t = torch.tensor([pos], **i32)
+    scale = 1 / 16
+    ws = _workspace(dev, 1)
+    out = torch.zeros((48, 1, 16, DIM), dtype=torch.int16, device=dev)
+    gk.check(gk.decode_step_layers_bf16(
+        out, q, k, v, caches["sk"], caches["sv"], s_pt, gk.make_config(*s_cfg), caches["gk"],
+        caches["gv"], g_pt, gk.make_config(*g_cfg), seq_t, pos_t, 0, 48, scale, 1, ws),
+        "decode_step")
+    torch.cuda.synchronize()
+    assert gk.decode_step_status(ws) == 0
+
+    ref = torch.zeros_like(out)
+    s_conf, g_conf = gk.make_config(*s_cfg), gk.make_config(*g_cfg)
+    s_split, s_n = gk.decode_split_plan(s_conf, 1, 1024)
+    g_split, g_n = gk.decode_split_plan(g_conf, 1, seq_len)
+    n = max(s_n, g_n)
+    pm = torch.empty(16 * n, device=dev)
+    pl = torch.empty(16 * n, device=dev)
+    pa = torch.empty(16 * n * DIM, device=dev)
+    si = gi = 0
+    for layer in range(48):
+        if is_global(layer):
+            conf, ck, cv, pt, cl, sp, ns = g_conf, ref_caches["gk"], ref_caches["gv"], g_pt, gi, g_split, g_n
+            gi += 1
+        else:
+            conf, ck, cv, pt, cl, sp, ns = s_conf, ref_caches["sk"], ref_caches["sv"], s_pt, si, s_split, s_n
+            si += 1
+        gk.check(gk.flash_attention_append_decode_paged_bf16(
+            ref[layer], pm, pl, pa, q[layer], ck, cv, pt, seq_t, pos_t, k[layer], v[layer],
+            conf, cl, scale, sp, ns, 1), "per-layer")
+    torch.cuda.synchronize()
+    for name in caches:
+        assert torch.equal(caches[name], ref_caches[name]), name
+    got = out.view(torch.bfloat16).float()
+    exp = ref.view(torch.bfloat16).float()
+    diff = (got - exp).abs()
+    denom = torch.maximum(torch.maximum(got.abs(), exp.abs()), torch.ones_like(got))
+    assert float(diff.max()) <= 2e-2 and float((diff / denom).max()) <= 1e-2
+    # A second step on the same workspace (the appended rows now in place).
+    out2 = torch.zeros_like(out)
+    gk.check(gk.decode_step_layers_bf16(
+        out2, q, k, v, caches["sk"], caches["sv"], s_pt, s_conf, caches["gk"], caches["gv"],
+        g_pt, g_conf, seq_t, pos_t, 0, 48, scale, 1, ws), "decode_step again")
+    torch.cuda.synchronize()
+    assert gk.decode_step_status(ws) == 0
+    assert torch.equal(out2, out)
