@@ -25,21 +25,27 @@
 //   splits = 32 / batch per (sequence, head) "unit". All splits of a unit
 //   therefore share one L2, and their partials are exchanged through it.
 //   compute waves 0..3: 8-key tiles t = wave, wave+4, ... of the split
-//   control wave 4:     waits for the previous layer, then combines the
-//                       unit's splits for its own 8-dim slices of the output
-//                       rows (slices c = s, s + splits, ...) and signals
+//   control wave 4:     waits for the previous layer, stages the layer's q
+//                       and appended K/V rows in LDS, then combines the
+//                       unit's splits for its own 8-dim output chunks
+//                       (c = s, s + splits, ...) and signals
+//   prefetch wave 5:    DMAs the next global layer's tiles 16..32 of the
+//                       split into LDS (global_load_lds), a few per barrier
+//                       interval over the 4 layers before it
 // A tile is 8 keys x 256 dims of K and V: lane (r, c) loads the 16-byte pack
 // c of key rows 4r..4r+3 (rows 0-3 for lanes 0-31, 4-7 for lanes 32-63).
+// Compute waves wait only for their own tile loads (q and the appended rows
+// come through LDS), so tiles prefetched long ahead never hold them up.
 //
 // Exchange between workgroups
-//   * split records (XCD-local): fp32 acc[2][256], (m, l)[2] per (layer
-//     parity, unit, split), written with ordinary stores (they reach the
-//     XCD's L2) and read with device-scope loads, which miss the L1 and are
-//     served from the L2 the writer shares. Empty dwords hold a
-//     signalling-NaN sentinel that arithmetic never produces, so readers
-//     poll the data itself. A writer empties its dwords one layer after
-//     they were combined; the parity continues across launches.
-//   * layer completion: each workgroup stores its output slices
+//   * split records (XCD-local): per (unit, split), 32 chunks of 8 output
+//     dims holding acc[8], m, l for each head of the pair, written with
+//     ordinary stores (they reach the XCD's L2) and read with sc0|nt loads,
+//     which skip the L1 and are served from the L2 the writer shares.
+//     Empty dwords hold a signalling-NaN sentinel that arithmetic never
+//     produces, so readers poll the data itself; the one reader of a chunk
+//     empties it again before it signals the layer complete.
+//   * layer completion: each workgroup stores its output chunks
 //     device-coherently, waits for them, then sets its XCD-local flag; the
 //     XCD's ticket-0 workgroup collects the 32 local flags and sets the XCD's
 //     device-coherent flag; every workgroup waits for all 8 XCD flags
@@ -67,7 +73,9 @@ constexpr int32_t kNumModelLayers = 48;
 constexpr int32_t kGlobalPeriod = 6;
 constexpr int kSHeads = 8, kSDim = 256, kSGroup = 2;
 constexpr int kComputeWaves = 4;
-constexpr int kStepThreads = (kComputeWaves + 1) * kWave;
+constexpr int kControlWave = kComputeWaves;      // wave 4
+constexpr int kPrefetchWave = kComputeWaves + 1; // wave 5
+constexpr int kStepThreads = (kComputeWaves + 2) * kWave;
 constexpr int kStepWorkgroups = 256;  // one workgroup per CU
 constexpr int kLPR = kSDim / kPackElems;      // 32 lanes per key row
 constexpr int kTileLoads = 4;                 // rows per lane per tile
@@ -77,18 +85,32 @@ constexpr int kSBits = 2;                     // log2(kLPR / kNP)
 constexpr int kWaveKeys = 128;                // row-table entries per wave
 constexpr int kMaxSplitKeys = kComputeWaves * kWaveKeys;
 constexpr int kRowElems = kSHeads * kSDim;
-constexpr int kRecordFloats = 2 * kSDim + 8;  // acc[2][256], m0 l0 m1 l1, pad
+// A split record is 32 chunks of 8 dims; a chunk holds, per head g of the
+// pair, acc[8] then (m, l) and 2 pad floats, so the reader of one chunk
+// finds everything it needs (and empties) in 96 contiguous bytes.
+constexpr int kChunks = kSDim / kPackElems;
+constexpr int kHalfChunk = kPackElems + 4;
+constexpr int kChunkFloats = 2 * kHalfChunk;
+constexpr int kRecordFloats = kChunks * kChunkFloats;
 constexpr int kXcds = 8;                      // XCDs of an MI355X
 constexpr int kXcdSlots = 32;                 // workgroups (CUs) per XCD
 constexpr int kMaxBatch = 8;                  // at least 4 splits per unit
 constexpr uint32_t kSentinel = 0x7fa5a5a5u;   // signalling NaN
-constexpr int kHeaderInts = 64;               // epoch, error, record parity, pad
-constexpr int kHeaderEpoch = 0, kHeaderError = 1, kHeaderParity = 2;
+constexpr int kHeaderInts = 64;               // epoch, error, pad
+constexpr int kHeaderEpoch = 0, kHeaderError = 1;
 constexpr int kTicketStride = 32;             // ints between the XCD ticket counters
 constexpr int kGlobalFlagStride = 16;         // ints per layer: one flag per XCD
-constexpr size_t kPadLds = 96 * 1024;         // dynamic LDS that keeps one workgroup per CU
 constexpr uint64_t kWaitTicks = 100ull * 1000 * 1000 / 5;  // 0.2 s at 100 MHz
 constexpr int kPrefetchTiles = 4;             // register tile buffers per wave
+// Global-layer tiles staged in LDS ahead of time by the prefetch wave: the
+// wave's tiles 16.. of a split (after the 16 held in compute-wave
+// registers). 17 x 8 KiB = 136 KiB of dynamic LDS, which also keeps the
+// hardware to one workgroup per CU.
+constexpr int kLdsSlots = 17;
+constexpr int kRegTiles = kComputeWaves * kPrefetchTiles;  // tiles 0..15 of a split: registers
+constexpr int kLdsLead = 4;                    // layers of lead for the LDS prefetch
+constexpr int kSlotsPerInterval = 2;           // slots requested between two barriers
+constexpr size_t kPadLds = (size_t)kLdsSlots * 2 * kTileLoads * kWave * 16;
 constexpr int kPolls = 3;                     // coherent polls in flight
 constexpr int kPollGap = 8;                   // s_sleep units (64 clocks) between them
 
@@ -165,22 +187,26 @@ __device__ __forceinline__ void local_store2(BufferRsrc r, int32_t off, float a,
 }
 
 // Everything a compute wave needs about one layer of its split.
+// All fields are wave-uniform.
 struct LayerView {
-  const uint16_t *kbase;  // cache K at (head, lane pack), row 0
-  const uint16_t *vbase;
-  uint16_t *append_k;     // cache row of the appended token (head, lane pack) or null
-  uint16_t *append_v;
+  int32_t kind;           // 0 sliding cache, 1 global cache
+  int32_t new_row;        // cache row this wave appends the new token to, or -1
   int32_t n_tiles;        // tiles of this wave
   bool owner;             // this wave attends over the new token
+  bool lds;               // tiles 16 .. 16 + kLdsSlots - 1 of the split are in LDS
+  int par;                // row table: s_rows[par]
 };
 
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p) {
-  __shared__ int4 s_rows[kComputeWaves][kWaveKeys / 4];
+  __shared__ int4 s_rows[2][kComputeWaves][kWaveKeys / 4];  // [layer parity][wave]
   __shared__ float s_prob[kComputeWaves][kWave];
   __shared__ float s_ml[kComputeWaves][kSGroup][2];
   __shared__ float s_acc[kComputeWaves][kSGroup][kSDim];
-
+  __shared__ uint4 s_q[kWave];    // q rows of the unit: [g][pack]
+  __shared__ uint4 s_new[kWave];  // appended rows of the unit: [K pack | V pack]
   __shared__ int32_t s_ticket;
+  __shared__ int4 s_lds_rows[kLdsSlots * kTileKeys / 4];  // cache rows of the LDS tiles
+  extern __shared__ uint4 s_tiles[];  // [slot][K 0..3 | V 0..3][lane]
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = wave_uniform(threadIdx.x / kWave);
@@ -189,7 +215,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     if (threadIdx.x == 0) p.probe[blockIdx.x] = xcd;
     return;
   }
-  if (threadIdx.x == kComputeWaves * kWave) {
+  if (threadIdx.x == kControlWave * kWave) {
     // Tickets count up forever; every launch takes exactly 32 per XCD.
     s_ticket = (int32_t)(__hip_atomic_fetch_add(p.tickets + xcd * kTicketStride, 1u,
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) %
@@ -207,17 +233,97 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   const int64_t q_stride = (int64_t)p.units * kSGroup * kSDim;  // per layer
   const int64_t kv_stride = (int64_t)p.units * kSDim;
   // Split records: one buffer over the whole region, addressed in bytes.
-  const BufferRsrc rec_buf =
-      buffer_of(p.records, 2ll * p.units * p.splits * kRecordFloats * 4);
-  // Record parity continues across launches (the header keeps it), so the
-  // record a layer writes was emptied one layer earlier, even for layer 0.
-  const int32_t epoch = coherent_load_i32(p.header + kHeaderEpoch) + 1;
-  const int32_t parity_base = coherent_load_i32(p.header + kHeaderParity);
-  auto record = [&](int32_t layer_i, int32_t s) -> int32_t {  // byte offset
-    return ((((parity_base + layer_i) & 1) * p.units + u) * p.splits + s) * (kRecordFloats * 4);
+  const BufferRsrc rec_buf = buffer_of(p.records, (int64_t)p.units * p.splits * kRecordFloats * 4);
+  auto record = [&](int32_t s) -> int32_t {  // byte offset of split s's record
+    return (u * p.splits + s) * (kRecordFloats * 4);
   };
+  const int32_t epoch = coherent_load_i32(p.header + kHeaderEpoch) + 1;
+  auto is_global_i = [&](int32_t i) { return model_layer_global(p.first_layer + i); };
 
-  if (wave == kComputeWaves) {
+  // Wave-local tile j of a split is tile t = wave + 4 j; tiles 0..15 are
+  // prefetched into compute-wave registers, tiles 16 .. 16 + kLdsSlots - 1
+  // of a global layer come from LDS slot t - 16, later ones are streamed.
+  if (wave == kPrefetchWave) {
+    // ----------------------------------------------------------- prefetch
+    // The LDS tiles of the next global layer are requested a few slots at a
+    // time over the kLdsLead layers before it, so the DMA traffic never
+    // arrives as one burst on the critical path of a layer. This wave waits
+    // only for its own DMA, so its outstanding loads hold nobody up.
+    auto next_global = [&](int32_t from) {
+      for (int32_t l = from; l < p.layer_count; ++l)
+        if (is_global_i(l)) return l;
+      return (int32_t)-1;
+    };
+    const int r = lane / kLPR;
+    const int64_t col = (int64_t)head * kSDim + (lane % kLPR) * kPackElems;
+    const uint16_t *kb = p.cache_k[1] + col;
+    const uint16_t *vb = p.cache_v[1] + col;
+    int32_t target = -1, slots = 0, filled = 0;
+    auto plan = [&](int32_t gi) {
+      // Cache rows of the slot keys: entry e = slot * 8 + key.
+      const Gemma4KvCacheConfig &c = p.c[1];
+      const int32_t cache_layer = wave_uniform(cache_layer_of(p.first_layer + gi));
+      const int32_t split_size = (seq_len + p.splits - 1) / p.splits;
+      const int32_t k0 = split * split_size;
+      const int32_t k1 = active ? min(seq_len, k0 + split_size) : k0;
+      const bool live_new = new_pos >= 0 && new_pos < seq_len;
+      const int32_t *pt = p.page_table[1] + b * c.max_pages_per_seq;
+      int32_t *tab = reinterpret_cast<int32_t *>(s_lds_rows);
+      for (int e = lane; e < kLdsSlots * kTileKeys; e += kWave) {
+        const int32_t key = k0 + (kRegTiles + e / kTileKeys) * kTileKeys + e % kTileKeys;
+        const int32_t logical = key / c.page_size;
+        const int32_t physical = pt[logical % c.max_pages_per_seq];
+        const bool ok = key < k1 && !(live_new && key == new_pos) && physical >= 0 &&
+                        physical < c.num_pages;
+        tab[e] = ok ? (cache_layer * c.num_pages + physical) * c.page_size +
+                          (key - logical * c.page_size)
+                    : kRowInvalid;
+      }
+      wave_lds_sync();
+      const int32_t tiles = k1 > k0 ? (k1 - k0 + kTileKeys - 1) / kTileKeys : 0;
+      target = gi;
+      slots = wave_uniform(max(0, min(kLdsSlots, tiles - kRegTiles)));
+      filled = 0;
+    };
+    auto request = [&](int count) {
+      for (int n = 0; n < count && filled < slots; ++n, ++filled) {
+        const int4 rr = s_lds_rows[filled * 2 + r];
+        const int32_t rows[4] = {rr.x, rr.y, rr.z, rr.w};
+#pragma unroll
+        for (int kl = 0; kl < kTileLoads; ++kl) {
+          const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems;
+          __builtin_amdgcn_global_load_lds(kb + off, s_tiles + (filled * 8 + kl) * kWave, 16, 0,
+                                           0);
+          __builtin_amdgcn_global_load_lds(vb + off, s_tiles + (filled * 8 + 4 + kl) * kWave, 16,
+                                           0, 0);
+        }
+      }
+    };
+    auto maybe_plan = [&](int32_t i) {  // at layer i: start the next global layer?
+      if (target > i) return;           // still filling for a later layer
+      const int32_t g = next_global(i + 1);
+      if (g >= 0 && g - i <= kLdsLead) plan(g);
+    };
+    maybe_plan(-1);
+    for (int32_t i = 0; i < p.layer_count; ++i) {
+      if (target == i) {
+        // Everything of this global layer requested and landed before its
+        // compute starts.
+        request(kLdsSlots);
+        wait_stores_complete();
+      }
+      __syncthreads();  // A
+      if (target > i) request(kSlotsPerInterval);
+      __syncthreads();  // B
+      if (target > i) request(kSlotsPerInterval);
+      __syncthreads();  // C
+      maybe_plan(i);
+      if (target > i) request(kSlotsPerInterval);
+    }
+    return;
+  }
+
+  if (wave == kControlWave) {
     // ------------------------------------------------------------ control
     bool abort = false;
     // A split longer than the row tables hold would drop keys: report it.
@@ -241,41 +347,61 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     };
     // Ticket 0 of each XCD: collect the XCD's 32 local flags, then raise
     // the XCD's device-wide flag.
+    const BufferRsrc local_buf =
+        buffer_of(p.local_flags, (int64_t)kNumModelLayers * kXcds * kXcdSlots * 4);
     auto publish_xcd = [&](int32_t layer_i) {
-      const int32_t *row = p.local_flags + (layer_i * kXcds + xcd) * kXcdSlots;
+      const int32_t off = ((layer_i * kXcds + xcd) * kXcdSlots + (lane & (kXcdSlots - 1))) * 4;
       const uint64_t t0 = now_ticks();
       while (!abort) {
         const bool ok = lane >= kXcdSlots ||
-                        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(
-                            buffer_of(row, kXcdSlots * 4), lane * 4, 0, kLocalLoadAux) == epoch;
+                        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(local_buf, off, 0,
+                                                                      kLocalLoadAux) == epoch;
         if (__ballot(!ok) == 0) break;
         if (now_ticks() - t0 > kWaitTicks) abort = true;
       }
       if (lane == 0) coherent_store_i32(p.global_flags + layer_i * kGlobalFlagStride + xcd, epoch);
     };
-    // Lane (sp, g) = (lane / 2, lane % 2) reads split sp's row g.
-    const int sp = lane >> 1;
-    const int g = lane & 1;
+    // Lane (g, sp) = (lane / 32, lane % 32) reads split sp's row g, so the
+    // reductions over splits stay within 32-lane halves (DPP row ops and
+    // one swizzle per step).
+    const int sp = lane & (kXcdSlots - 1);
+    const int g = lane >> 5;
+    const bool live = sp < p.splits;
+    const BufferRsrc in_buf_q = buffer_of(p.q, (int64_t)p.layer_count * q_stride * 2);
+    const BufferRsrc in_buf_k = buffer_of(p.new_k, (int64_t)p.layer_count * kv_stride * 2);
+    const BufferRsrc in_buf_v = buffer_of(p.new_v, (int64_t)p.layer_count * kv_stride * 2);
     for (int32_t i = 0; i < p.layer_count; ++i) {
       if (i > 0) wait_layer(i - 1);
+      // Layer i's inputs exist only now: q rows and appended K/V rows of the
+      // unit, read device-coherently and staged in LDS for the compute waves.
+      {
+        const int32_t qoff = (int32_t)((i * q_stride + (u * kSGroup + (lane >> 5)) * kSDim +
+                                        (lane & 31) * kPackElems) * 2);
+        const int32_t kvoff = (int32_t)((i * kv_stride + u * kSDim + (lane & 31) * kPackElems) * 2);
+        const u32x4 qv = __builtin_amdgcn_raw_buffer_load_b128(in_buf_q, qoff, 0, kCoherentAux);
+        const u32x4 nv = lane < 32
+                             ? __builtin_amdgcn_raw_buffer_load_b128(in_buf_k, kvoff, 0, kCoherentAux)
+                             : __builtin_amdgcn_raw_buffer_load_b128(in_buf_v, kvoff, 0, kCoherentAux);
+        s_q[lane] = make_uint4(qv[0], qv[1], qv[2], qv[3]);
+        s_new[lane] = make_uint4(nv[0], nv[1], nv[2], nv[3]);
+      }
       __syncthreads();  // A: layer i may start
       __syncthreads();  // B: this workgroup's compute waves finished layer i
 
       // Combine unit u's splits for the 8-dim chunks c = split, split +
-      // splits, ... of both rows: one round of L2 loads per chunk.
-      for (int32_t c = split; active && c < kSDim / kPackElems; c += p.splits) {
+      // splits, ... of both rows: one round of L2 loads per chunk; the
+      // chunk is emptied again right after it is read.
+      for (int32_t c = split; active && c < kChunks; c += p.splits) {
         // Lanes past the live splits read split 0 and weigh it zero.
-        const int32_t rec = record(i, sp < p.splits ? sp : 0);
-        const int32_t ml_off = rec + (2 * kSDim + 2 * g) * 4;
-        const int32_t acc_off = rec + (g * kSDim + c * kPackElems) * 4;
+        const int32_t off = record(live ? sp : 0) + (c * kChunkFloats + g * kHalfChunk) * 4;
         struct Poll {
-          u32x2 ml;
           u32x4 lo, hi;
+          u32x2 ml;
         };
         auto issue = [&](Poll &q) {
-          q.ml = __builtin_amdgcn_raw_buffer_load_b64(rec_buf, ml_off, 0, kLocalLoadAux);
-          q.lo = __builtin_amdgcn_raw_buffer_load_b128(rec_buf, acc_off, 0, kLocalLoadAux);
-          q.hi = __builtin_amdgcn_raw_buffer_load_b128(rec_buf, acc_off + 16, 0, kLocalLoadAux);
+          q.lo = __builtin_amdgcn_raw_buffer_load_b128(rec_buf, off, 0, kLocalLoadAux);
+          q.hi = __builtin_amdgcn_raw_buffer_load_b128(rec_buf, off + 16, 0, kLocalLoadAux);
+          q.ml = __builtin_amdgcn_raw_buffer_load_b64(rec_buf, off + 32, 0, kLocalLoadAux);
         };
         auto complete = [&](const Poll &q) {
           bool bad = q.ml[0] == kSentinel || q.ml[1] == kSentinel;
@@ -310,65 +436,41 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
           }
         }
         auto finish = [&](const Poll &got) {
-        const bool live = sp < p.splits;
-        const float m_s = live ? __uint_as_float(got.ml[0]) : -INFINITY;
-        const float l_s = live ? __uint_as_float(got.ml[1]) : 0.0f;
-        // Reduce over the splits (lane bits 1..5) of each row g = lane bit 0.
-        float big_m = m_s;
-        big_m = fmaxf(big_m, lane_xor<2>(big_m));
-        big_m = fmaxf(big_m, lane_xor<4>(big_m));
-        big_m = fmaxf(big_m, lane_xor<8>(big_m));
-        big_m = fmaxf(big_m, lane_xor<16>(big_m));
-        big_m = fmaxf(big_m, lane_xor<32>(big_m));
-        const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
-        const float w = l_s > 0.0f ? __builtin_amdgcn_exp2f(m_s - m_ref) : 0.0f;
-        float big_l = w * l_s;
-        big_l += lane_xor<2>(big_l);
-        big_l += lane_xor<4>(big_l);
-        big_l += lane_xor<8>(big_l);
-        big_l += lane_xor<16>(big_l);
-        big_l += lane_xor<32>(big_l);
-        // Value-splitting sum of the 8 weighted dims: after the exchanges
-        // over lane bits 5, 4, 3 each lane holds the full sum of dim
-        // 4*b5 + 2*b4 + b3; bits 2 and 1 are then summed in place.
-        float v[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[j] = w * __uint_as_float(got.lo[j]);
-          v[4 + j] = w * __uint_as_float(got.hi[j]);
-        }
-        {
-          const bool h = lane & 32;
+          const float m_s = live ? __uint_as_float(got.ml[0]) : -INFINITY;
+          const float l_s = live ? __uint_as_float(got.ml[1]) : 0.0f;
+          // Reduce over the splits (lane bits 0..4) of each row g = lane bit 5.
+          float big_m = m_s;
+          big_m = fmaxf(big_m, lane_pair<16>(big_m));
+          big_m = fmaxf(big_m, lane_pair<8>(big_m));
+          big_m = fmaxf(big_m, lane_pair<4>(big_m));
+          big_m = fmaxf(big_m, lane_pair<2>(big_m));
+          big_m = fmaxf(big_m, lane_pair<1>(big_m));
+          const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
+          const float w = l_s > 0.0f ? __builtin_amdgcn_exp2f(m_s - m_ref) : 0.0f;
+          float big_l = w * l_s;
+          big_l += lane_pair<16>(big_l);
+          big_l += lane_pair<8>(big_l);
+          big_l += lane_pair<4>(big_l);
+          big_l += lane_pair<2>(big_l);
+          big_l += lane_pair<1>(big_l);
+          // Value-splitting sum of the 8 weighted dims over the 32 split
+          // lanes: lane holds the sum of dim (lane >> 2) & 7 afterwards.
+          float v[8];
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float send = h ? v[j] : v[j + 4];
-            v[j] = (h ? v[j + 4] : v[j]) + lane_xor<32>(send);
+            v[j] = w * __uint_as_float(got.lo[j]);
+            v[4 + j] = w * __uint_as_float(got.hi[j]);
           }
-        }
-        {
-          const bool h = lane & 16;
-#pragma unroll
-          for (int j = 0; j < 2; ++j) {
-            const float send = h ? v[j] : v[j + 2];
-            v[j] = (h ? v[j + 2] : v[j]) + lane_xor<16>(send);
+          split_butterfly<8, 16>(v, lane);
+          if ((lane & 3) == 0) {
+            const int dim = (lane >> 2) & 7;
+            const float inv = big_l > 0.0f ? 1.0f / big_l : 0.0f;
+            // Output rows go out device-coherent.
+            const BufferRsrc out_buf = buffer_of(p.out + i * q_stride, q_stride * 2);
+            __builtin_amdgcn_raw_buffer_store_b16(
+                (uint16_t)f32_to_bf16_bits(v[0] * inv), out_buf,
+                ((u * kSGroup + g) * kSDim + c * kPackElems + dim) * 2, 0, kCoherentAux);
           }
-        }
-        {
-          const bool h = lane & 8;
-          const float send = h ? v[0] : v[1];
-          v[0] = (h ? v[1] : v[0]) + lane_xor<8>(send);
-        }
-        v[0] += lane_xor<4>(v[0]);
-        v[0] += lane_xor<2>(v[0]);
-        if ((lane & 6) == 0) {
-          const int dim = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
-          const float inv = big_l > 0.0f ? 1.0f / big_l : 0.0f;
-          // Output rows go out device-coherent.
-          const BufferRsrc out_buf = buffer_of(p.out + i * q_stride, q_stride * 2);
-          __builtin_amdgcn_raw_buffer_store_b16(
-              (uint16_t)f32_to_bf16_bits(v[0] * inv), out_buf,
-              ((u * kSGroup + g) * kSDim + c * kPackElems + dim) * 2, 0, kCoherentAux);
-        }
         };
         static_assert(kPolls == 3, "one reduction copy per poll slot");
         if (found == 1) {
@@ -378,24 +480,29 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         } else {
           finish(polls[0]);
         }
+        if (live) {
+          // Empty the chunk for the next layer (completed before this
+          // workgroup's flag, so before any next-layer write).
+          const u32x4 s4 = {kSentinel, kSentinel, kSentinel, kSentinel};
+          const u32x2 s2 = {kSentinel, kSentinel};
+          __builtin_amdgcn_raw_buffer_store_b128(s4, rec_buf, off, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b128(s4, rec_buf, off + 16, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b64(s2, rec_buf, off + 32, 0, 0);
+        }
       }
       __syncthreads();  // C: records read; compute waves may prefetch
-      // My output slices are complete (device-wide) before my local flag.
+      // My output slices and chunk resets are complete before my local flag.
       wait_stores_complete();
       if (lane == 0) {
-        __builtin_amdgcn_raw_buffer_store_b32(
-            (uint32_t)epoch, buffer_of(p.local_flags, (int64_t)kNumModelLayers * kXcds * kXcdSlots * 4),
-            ((i * kXcds + xcd) * kXcdSlots + ticket) * 4, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)epoch, local_buf,
+                                              ((i * kXcds + xcd) * kXcdSlots + ticket) * 4, 0, 0);
       }
       if (ticket == 0) publish_xcd(i);
     }
     if (xcd == 0 && ticket == 0) {
       // Every workgroup has read the header (and finished): advance it.
       wait_layer(p.layer_count - 1);
-      if (lane == 0) {
-        coherent_store_i32(p.header + kHeaderParity, (parity_base + p.layer_count) & 1);
-        coherent_store_i32(p.header + kHeaderEpoch, epoch);
-      }
+      if (lane == 0) coherent_store_i32(p.header + kHeaderEpoch, epoch);
     }
     if (abort && lane == 0) coherent_store_i32(p.header + kHeaderError, 1);
     return;
@@ -409,7 +516,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   const int my_kl = idx / kSGroup;
 
   // Layer view + row table for layer i of this split and wave: keys of the
-  // wave's tiles go to s_rows[wave] in tile order (tile i at 8i, key 4r+kl).
+  // wave's tiles go to s_rows[i & 1][wave] in tile order (tile j at 8j,
+  // key 4r+kl).
   auto setup = [&](int32_t i) -> LayerView {
     LayerView v;
     const int32_t layer = p.first_layer + i;
@@ -433,11 +541,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                                 ? append_row(c, p.page_table[kind], cache_layer, b, new_pos)
                                 : -1;
     v.owner = live_new && split == owner_split && wave == owner_wave;
-    const int64_t col = (int64_t)head * kSDim + cpack * kPackElems;
-    v.kbase = p.cache_k[kind] + col;
-    v.vbase = p.cache_v[kind] + col;
-    v.append_k = new_row >= 0 ? p.cache_k[kind] + (int64_t)new_row * kRowElems + col : nullptr;
-    v.append_v = new_row >= 0 ? p.cache_v[kind] + (int64_t)new_row * kRowElems + col : nullptr;
+    v.lds = kind == 1;
+    v.par = i & 1;
+    v.kind = kind;
+    v.new_row = wave_uniform(new_row);
     // Two table entries per lane: wave-local key e = lane, lane + 64.
     const int32_t *pt = p.page_table[kind] + b * c.max_pages_per_seq;
     int32_t rows[2];
@@ -454,7 +561,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                       (key - logical * c.page_size))
                    : kRowInvalid;
     }
-    int32_t *tab = reinterpret_cast<int32_t *>(s_rows[wave]);
+    int32_t *tab = reinterpret_cast<int32_t *>(s_rows[v.par][wave]);
     tab[lane] = rows[0];
     tab[lane + kWave] = rows[1];
     wave_lds_sync();
@@ -465,26 +572,34 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     uint4 k[kTileLoads], v[kTileLoads];
     uint32_t valid;
   };
+  const int32_t col = head * kSDim + cpack * kPackElems;  // element offset in a cache row
   auto issue = [&](TileBuf &tb, const LayerView &v, int t) {
-    const int4 rr = s_rows[wave][t * 2 + r];
+    const int4 rr = s_rows[v.par][wave][t * 2 + r];
     const int32_t rows[4] = {rr.x, rr.y, rr.z, rr.w};
+    const uint16_t *kb = p.cache_k[v.kind];
+    const uint16_t *vb = p.cache_v[v.kind];
     tb.valid = 0;
 #pragma unroll
     for (int kl = 0; kl < kTileLoads; ++kl) {
       tb.valid |= (rows[kl] >= 0 ? 1u : 0u) << kl;
-      const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems;
-      tb.k[kl] = load128(v.kbase + off);
-      tb.v[kl] = load128(v.vbase + off);
+      const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems + col;
+      tb.k[kl] = load128(kb + off);
+      tb.v[kl] = load128(vb + off);
     }
   };
 
   uint32_t qw[kSGroup][4];
   float m[kSGroup], acc[kSGroup][8], l_lane;
-  auto compute = [&](const TileBuf &t) {
+  // One tile in two steps, so a tile read from LDS needs its V packs in
+  // registers only after the K packs are done with: scores() updates the
+  // online softmax and leaves the tile's probabilities in pv / alpha;
+  // accumulate() adds P.V.
+  float pv[kNP], alpha[kSGroup];
+  auto scores = [&](const uint4 (&k)[kTileLoads], uint32_t valid_bits) {
     float part[kNP];
 #pragma unroll
     for (int kl = 0; kl < kTileLoads; ++kl) {
-      const uint32_t kw[4] = {t.k[kl].x, t.k[kl].y, t.k[kl].z, t.k[kl].w};
+      const uint32_t kw[4] = {k[kl].x, k[kl].y, k[kl].z, k[kl].w};
 #pragma unroll
       for (int g = 0; g < kSGroup; ++g) {
         float a = 0.0f;
@@ -494,11 +609,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
     }
     split_butterfly<kNP, kLPR / 2>(part, lane);
-    const bool valid = (t.valid >> my_kl) & 1u;
+    const bool valid = (valid_bits >> my_kl) & 1u;
     const float score = valid ? part[0] * p.q_scale : -INFINITY;
     float tmax[kSGroup];
     gather_heads<kSGroup, kSBits>(reduce_max_from<(1 << kSBits) * kSGroup>(score), my_g, tmax);
-    float alpha[kSGroup], m_use[kSGroup];
+    float m_use[kSGroup];
 #pragma unroll
     for (int g = 0; g < kSGroup; ++g) {
       const float m_new = fmaxf(m[g], tmax[g]);
@@ -512,12 +627,13 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     l_lane = l_lane * my_alpha + prob;
     s_prob[wave][r * kNP + idx] = prob;
     wave_lds_sync();
-    float pv[kNP];
 #pragma unroll
     for (int i = 0; i < kNP; i += 4) {
       const float4 q4 = *reinterpret_cast<const float4 *>(&s_prob[wave][r * kNP + i]);
       pv[i] = q4.x; pv[i + 1] = q4.y; pv[i + 2] = q4.z; pv[i + 3] = q4.w;
     }
+  };
+  auto accumulate = [&](const uint4 (&v)[kTileLoads], uint32_t valid_bits) {
 #pragma unroll
     for (int g = 0; g < kSGroup; ++g) {
 #pragma unroll
@@ -526,7 +642,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
 #pragma unroll
     for (int kl = 0; kl < kTileLoads; ++kl) {
       float vf[8];
-      const uint4 vp = (t.valid >> kl) & 1u ? t.v[kl] : make_uint4(0, 0, 0, 0);
+      const uint4 vp = (valid_bits >> kl) & 1u ? v[kl] : make_uint4(0, 0, 0, 0);
       unpack8(vp, vf);
 #pragma unroll
       for (int g = 0; g < kSGroup; ++g) {
@@ -536,65 +652,114 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
     }
   };
+  auto compute = [&](const TileBuf &t) {
+    scores(t.k, t.valid);
+    accumulate(t.v, t.valid);
+  };
 
+  // Register prefetch. At the end of layer i (barrier C) the first four
+  // tiles of layer i+1 are issued. When layer i+2 is global and layer i+1
+  // needs only buffer 0, layer i+2's tiles 1..3 are issued there too (after
+  // layer i+1's tile, so waiting for that one never waits for them), and
+  // its tile 0 follows at the end of layer i+1.
   TileBuf buf[kPrefetchTiles];
-  LayerView view = setup(0);
+  LayerView cur, nxt;
+  bool nxt_ready = false;  // nxt holds layer i+1 with tiles 1..3 in flight
+  auto prepare = [&](int32_t i) {  // at the end of layer i (i = -1: start)
+    const int32_t n1 = i + 1, n2 = i + 2;
+    if (n1 >= p.layer_count) return;
+    const bool early = nxt_ready;  // layer n1's tiles 1..3 already in flight
+    const LayerView v1 = early ? nxt : setup(n1);
+    const bool early2 =
+        n2 < p.layer_count && is_global_i(n2) && !is_global_i(n1) && v1.n_tiles <= 1;
+    if (early2) nxt = setup(n2);
+    // Each buffer is written once, in buffer order, so layer n1's tile 0
+    // always precedes layer n2's tiles.
 #pragma unroll
-  for (int j = 0; j < kPrefetchTiles; ++j)
-    if (j < view.n_tiles) issue(buf[j], view, j);
+    for (int j = 0; j < kPrefetchTiles; ++j) {
+      const bool for_n2 = early2 && j >= 1 && j < nxt.n_tiles;
+      const bool for_n1 = j < v1.n_tiles && (j == 0 || !early);
+      if (for_n2) {
+        issue(buf[j], nxt, j);
+      } else if (for_n1) {
+        issue(buf[j], v1, j);
+      }
+    }
+    nxt_ready = early2;
+    cur = v1;
+  };
+  prepare(-1);
 
-  // This wave's record dwords: head g = lane / 32, dims d, d+1 of its quarter.
+  // This wave's record dwords: head g = lane / 32, dims d, d+1 of its
+  // quarter, inside 8-dim chunk d / 8 (whose first lane also writes m, l).
   const int rec_g = lane / kLPR;
   const int rec_d = wave * (kSDim / kComputeWaves) + (lane % kLPR) * 2;
+  const int32_t rec_acc = (rec_d / kPackElems * kChunkFloats + rec_g * kHalfChunk + rec_d % kPackElems) * 4;
+  const int32_t rec_ml = (rec_d / kPackElems * kChunkFloats + rec_g * kHalfChunk + kPackElems) * 4;
 
   for (int32_t i = 0; i < p.layer_count; ++i) {
-    __syncthreads();  // A: layer i-1 published (or i == 0)
-    if (active) {
-      // Layer i-1's record (for i == 0 the previous launch's last one) has
-      // been combined by every reader: reset my dwords to empty.
-      const int32_t rec = record(i - 1, split);
-      const float sf = __uint_as_float(kSentinel);
-      local_store2(rec_buf, rec + (rec_g * kSDim + rec_d) * 4, sf, sf);
-      if (wave == 0 && (lane & (kLPR - 1)) == 0)
-        local_store2(rec_buf, rec + (2 * kSDim + 2 * rec_g) * 4, sf, sf);
-    }
-    // q rows of the two query heads of this kv head, packed bf16.
-    const uint16_t *qrow = p.q + i * q_stride + (int64_t)u * kSGroup * kSDim + cpack * kPackElems;
+    __syncthreads();  // A: layer i-1 published (or i == 0), inputs in LDS
+    const LayerView view = cur;
 #pragma unroll
     for (int g = 0; g < kSGroup; ++g) {
-      const uint4 qp = load128(qrow + g * kSDim);
+      const uint4 qp = s_q[g * kLPR + cpack];
       qw[g][0] = qp.x; qw[g][1] = qp.y; qw[g][2] = qp.z; qw[g][3] = qp.w;
       m[g] = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
     }
     l_lane = 0.0f;
-    uint4 nk = make_uint4(0, 0, 0, 0), nv = nk;
-    const bool appender = view.append_k != nullptr;
-    if (view.owner || appender) {
-      const int64_t src = i * kv_stride + (int64_t)u * kSDim + cpack * kPackElems;
-      nk = load128(p.new_k + src);
-      nv = load128(p.new_v + src);
-    }
-
-    for (int32_t t0 = 0; t0 < view.n_tiles; t0 += kPrefetchTiles) {
+    {
+      // Wave-local tiles: [0, 4) in registers, [4, lds_end) in LDS (global
+      // layers), [lds_end, n) streamed through the register buffers, which
+      // are refilled as the prefetched tiles are consumed.
+      const int32_t n = view.n_tiles;
+      int32_t lds_end = kPrefetchTiles;
+      if (view.lds) {
+        while (lds_end < n && wave + kComputeWaves * lds_end < kRegTiles + kLdsSlots) ++lds_end;
+      }
+      const int32_t n_stream = n > lds_end ? n - lds_end : 0;
 #pragma unroll
       for (int j = 0; j < kPrefetchTiles; ++j) {
-        if (t0 + j < view.n_tiles) compute(buf[j]);
-        if (t0 + j + kPrefetchTiles < view.n_tiles) issue(buf[j], view, t0 + j + kPrefetchTiles);
+        if (j < n) compute(buf[j]);
+        if (j < n_stream) issue(buf[j], view, lds_end + j);
+      }
+      for (int32_t j = kPrefetchTiles; j < lds_end; ++j) {
+        const int slot = wave + kComputeWaves * j - kRegTiles;
+        const int4 rr = s_lds_rows[slot * 2 + r];
+        const uint32_t valid = (rr.x >= 0 ? 1u : 0u) | (rr.y >= 0 ? 2u : 0u) |
+                               (rr.z >= 0 ? 4u : 0u) | (rr.w >= 0 ? 8u : 0u);
+        uint4 kv[kTileLoads];
+#pragma unroll
+        for (int kl = 0; kl < kTileLoads; ++kl) kv[kl] = s_tiles[(slot * 8 + kl) * kWave + lane];
+        scores(kv, valid);
+#pragma unroll
+        for (int kl = 0; kl < kTileLoads; ++kl) kv[kl] = s_tiles[(slot * 8 + 4 + kl) * kWave + lane];
+        accumulate(kv, valid);
+      }
+      for (int32_t t0 = 0; t0 < n_stream; t0 += kPrefetchTiles) {
+#pragma unroll
+        for (int j = 0; j < kPrefetchTiles; ++j) {
+          if (t0 + j < n_stream) compute(buf[j]);
+          if (t0 + j + kPrefetchTiles < n_stream)
+            issue(buf[j], view, lds_end + t0 + j + kPrefetchTiles);
+        }
       }
     }
     if (view.owner) {
       // The appended token: row 0 of a one-key tile, read from new K/V.
       TileBuf nt;
+      const uint4 nk = s_new[cpack];
+      const uint4 nv = s_new[kLPR + cpack];
 #pragma unroll
       for (int kl = 0; kl < kTileLoads; ++kl) { nt.k[kl] = nk; nt.v[kl] = nv; }
       nt.valid = r == 0 ? 1u : 0u;
       compute(nt);
     }
-    if (appender && r == 0) {
-      store128(view.append_k, nk);
-      store128(view.append_v, nv);
+    if (view.new_row >= 0 && r == 0) {
+      const int64_t dst = (int64_t)view.new_row * kRowElems + col;
+      store128(p.cache_k[view.kind] + dst, s_new[cpack]);
+      store128(p.cache_v[view.kind] + dst, s_new[kLPR + cpack]);
     }
 
     // Wave totals to LDS, then the four waves' partials are merged.
@@ -621,7 +786,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
     }
     __syncthreads();  // B
-    {
+    if (active) {
       float big_m = -INFINITY;
 #pragma unroll
       for (int w = 0; w < kComputeWaves; ++w) big_m = fmaxf(big_m, s_ml[w][rec_g][0]);
@@ -635,25 +800,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         a0 = fmaf(a.x, f, a0);
         a1 = fmaf(a.y, f, a1);
       }
-      // My reset of these dwords (one layer ago) must land before the data.
-      wait_stores_complete();
-      if (active) {
-        const int32_t rec = record(i, split);
-        local_store2(rec_buf, rec + (rec_g * kSDim + rec_d) * 4, a0, a1);
-        if (wave == 0 && (lane & (kLPR - 1)) == 0)
-          local_store2(rec_buf, rec + (2 * kSDim + 2 * rec_g) * 4, big_m, big_l);
-      }
+      // The chunk was emptied by its reader before the previous layer
+      // completed, so these stores need no wait.
+      const int32_t rec = record(split);
+      local_store2(rec_buf, rec + rec_acc, a0, a1);
+      if (rec_d % kPackElems == 0) local_store2(rec_buf, rec + rec_ml, big_m, big_l);
     }
-    // C: the control wave has read the split records. The next layer's
-    // tiles are issued only now, so their HBM traffic does not queue ahead
-    // of the record reads on this layer's critical path.
-    __syncthreads();
-    if (i + 1 < p.layer_count) {
-      view = setup(i + 1);
-#pragma unroll
-      for (int j = 0; j < kPrefetchTiles; ++j)
-        if (j < view.n_tiles) issue(buf[j], view, j);
-    }
+    __syncthreads();  // C: the control wave has read the split records
+    prepare(i);
   }
 }
 
@@ -681,7 +835,7 @@ WorkspaceLayout workspace_layout(int32_t batch_count) {
   w.global_flags = w.local_flags + (int64_t)kNumModelLayers * kXcds * kXcdSlots;
   w.probe = w.global_flags + (int64_t)kNumModelLayers * kGlobalFlagStride;
   w.int_count = w.probe + kStepWorkgroups;
-  w.record_floats = 2ll * w.units * w.splits * kRecordFloats;
+  w.record_floats = (int64_t)w.units * w.splits * kRecordFloats;
   w.bytes = (w.int_count + w.record_floats) * 4;
   return w;
 }
