@@ -198,7 +198,9 @@ struct LayerView {
 };
 
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p) {
-  __shared__ int4 s_rows[2][kComputeWaves][kWaveKeys / 4];  // [layer parity][wave]
+  // Row tables [slot][wave]: slots 0/1 by layer parity, slot 2 for a
+  // global layer whose tiles are requested early.
+  __shared__ int4 s_rows[3][kComputeWaves][kWaveKeys / 4];
   __shared__ float s_prob[kComputeWaves][kWave];
   __shared__ float s_ml[kComputeWaves][kSGroup][2];
   __shared__ float s_acc[kComputeWaves][kSGroup][kSDim];
@@ -518,7 +520,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   // Layer view + row table for layer i of this split and wave: keys of the
   // wave's tiles go to s_rows[i & 1][wave] in tile order (tile j at 8j,
   // key 4r+kl).
-  auto setup = [&](int32_t i) -> LayerView {
+  auto setup = [&](int32_t i, int slot) -> LayerView {
     LayerView v;
     const int32_t layer = p.first_layer + i;
     const int kind = model_layer_global(layer) ? 1 : 0;
@@ -542,7 +544,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                                 : -1;
     v.owner = live_new && split == owner_split && wave == owner_wave;
     v.lds = kind == 1;
-    v.par = i & 1;
+    v.par = slot;
     v.kind = kind;
     v.new_row = wave_uniform(new_row);
     // Two table entries per lane: wave-local key e = lane, lane + 64.
@@ -657,35 +659,47 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     accumulate(t.v, t.valid);
   };
 
-  // Register prefetch. At the end of layer i (barrier C) the first four
-  // tiles of layer i+1 are issued. When layer i+2 is global and layer i+1
-  // needs only buffer 0, layer i+2's tiles 1..3 are issued there too (after
-  // layer i+1's tile, so waiting for that one never waits for them), and
-  // its tile 0 follows at the end of layer i+1.
+  // Register prefetch. At the end of layer i (barrier C) the tiles of layer
+  // i+1 are issued. A global layer g's first four tiles are spread out
+  // instead when the sliding layers before it use only buffer 0: tile j of
+  // g is issued at the end of layer g-5+j (tiles 1, 2, 3 three, two and one
+  // layers ahead, tile 0 last), each after that layer's own tile, so the
+  // wait for a layer's tile never waits for them and no end of layer issues
+  // more than two tiles' worth of loads.
   TileBuf buf[kPrefetchTiles];
-  LayerView cur, nxt;
-  bool nxt_ready = false;  // nxt holds layer i+1 with tiles 1..3 in flight
+  LayerView cur, pend;
+  int32_t pend_layer = -1;  // global layer whose tiles are being issued early
+  int pend_next = 1;        // next early tile of pend_layer to issue
   auto prepare = [&](int32_t i) {  // at the end of layer i (i = -1: start)
-    const int32_t n1 = i + 1, n2 = i + 2;
+    const int32_t n1 = i + 1;
     if (n1 >= p.layer_count) return;
-    const bool early = nxt_ready;  // layer n1's tiles 1..3 already in flight
-    const LayerView v1 = early ? nxt : setup(n1);
-    const bool early2 =
-        n2 < p.layer_count && is_global_i(n2) && !is_global_i(n1) && v1.n_tiles <= 1;
-    if (early2) nxt = setup(n2);
-    // Each buffer is written once, in buffer order, so layer n1's tile 0
-    // always precedes layer n2's tiles.
+    const bool from_pend = n1 == pend_layer;
+    const LayerView v1 = from_pend ? pend : setup(n1, n1 & 1);
+    // A later global layer within reach of the early scheme?
+    int32_t g = -1;
+    for (int32_t l = n1 + 1; l < p.layer_count && l <= n1 + kPrefetchTiles - 1; ++l) {
+      if (is_global_i(l)) { g = l; break; }
+    }
+    const bool early = g >= 0 && !is_global_i(n1) && v1.n_tiles <= 1;
+    if (early && pend_layer != g) {
+      pend = setup(g, 2);
+      pend_layer = g;
+      pend_next = 1;
+    }
+    // Early tiles of g due by now: j <= kPrefetchTiles - (g - n1).
+    const int due = early ? kPrefetchTiles - (g - n1) : 0;
 #pragma unroll
     for (int j = 0; j < kPrefetchTiles; ++j) {
-      const bool for_n2 = early2 && j >= 1 && j < nxt.n_tiles;
-      const bool for_n1 = j < v1.n_tiles && (j == 0 || !early);
-      if (for_n2) {
-        issue(buf[j], nxt, j);
+      const bool for_pend = early && j >= pend_next && j <= due && j < pend.n_tiles;
+      const bool for_n1 = j < v1.n_tiles && (!from_pend || j == 0 || j >= pend_next);
+      if (for_pend) {
+        issue(buf[j], pend, j);
       } else if (for_n1) {
         issue(buf[j], v1, j);
       }
     }
-    nxt_ready = early2;
+    if (early) pend_next = max(pend_next, due + 1);
+    if (from_pend) pend_layer = -1;
     cur = v1;
   };
   prepare(-1);
