@@ -111,8 +111,6 @@ constexpr int kRegTiles = kComputeWaves * kPrefetchTiles;  // tiles 0..15 of a s
 constexpr int kLdsLead = 4;                    // layers of lead for the LDS prefetch
 constexpr int kSlotsPerInterval = 2;           // slots requested between two barriers
 constexpr size_t kPadLds = (size_t)kLdsSlots * 2 * kTileLoads * kWave * 16;
-constexpr int kPolls = 3;                     // coherent polls in flight
-constexpr int kPollGap = 8;                   // s_sleep units (64 clocks) between them
 
 struct StepParams {
   uint16_t *out;
@@ -198,9 +196,7 @@ struct LayerView {
 };
 
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p) {
-  // Row tables [slot][wave]: slots 0/1 by layer parity, slot 2 for a
-  // global layer whose tiles are requested early.
-  __shared__ int4 s_rows[3][kComputeWaves][kWaveKeys / 4];
+  __shared__ int4 s_rows[2][kComputeWaves][kWaveKeys / 4];  // [layer parity][wave]
   __shared__ float s_prob[kComputeWaves][kWave];
   __shared__ float s_ml[kComputeWaves][kSGroup][2];
   __shared__ float s_acc[kComputeWaves][kSGroup][kSDim];
@@ -411,33 +407,18 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
           for (int j = 0; j < 4; ++j) bad |= q.lo[j] == kSentinel || q.hi[j] == kSentinel;
           return __ballot(bad) == 0;
         };
-        Poll polls[kPolls];
-#pragma unroll
-        for (int k = 0; k < kPolls; ++k) {
-          issue(polls[k]);
-          if (k + 1 < kPolls) __builtin_amdgcn_s_sleep(kPollGap);
-        }
-        // Wave-uniform index of the first complete poll. Each outcome gets
-        // its own copy of the reduction below, so only that poll's registers
-        // are read (the loads still in flight are never waited for).
-        int found = -1;
+        // One poll in flight at a time: measured faster than keeping
+        // several staggered polls outstanding.
+        Poll got;
         {
           const uint64_t t0 = now_ticks();
-          while (found < 0 && !abort) {
-#pragma unroll
-            for (int k = 0; k < kPolls; ++k) {
-              if (found < 0) {
-                if (complete(polls[k])) {
-                  found = k;
-                } else {
-                  issue(polls[k]);
-                }
-              }
-            }
-            if (found < 0 && now_ticks() - t0 > kWaitTicks) abort = true;
+          issue(got);
+          while (!complete(got) && !abort) {
+            if (now_ticks() - t0 > kWaitTicks) abort = true;
+            issue(got);
           }
         }
-        auto finish = [&](const Poll &got) {
+        {
           const float m_s = live ? __uint_as_float(got.ml[0]) : -INFINITY;
           const float l_s = live ? __uint_as_float(got.ml[1]) : 0.0f;
           // Reduce over the splits (lane bits 0..4) of each row g = lane bit 5.
@@ -473,14 +454,6 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                 (uint16_t)f32_to_bf16_bits(v[0] * inv), out_buf,
                 ((u * kSGroup + g) * kSDim + c * kPackElems + dim) * 2, 0, kCoherentAux);
           }
-        };
-        static_assert(kPolls == 3, "one reduction copy per poll slot");
-        if (found == 1) {
-          finish(polls[1]);
-        } else if (found == 2) {
-          finish(polls[2]);
-        } else {
-          finish(polls[0]);
         }
         if (live) {
           // Empty the chunk for the next layer (completed before this
@@ -659,48 +632,19 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     accumulate(t.v, t.valid);
   };
 
-  // Register prefetch. At the end of layer i (barrier C) the tiles of layer
-  // i+1 are issued. A global layer g's first four tiles are spread out
-  // instead when the sliding layers before it use only buffer 0: tile j of
-  // g is issued at the end of layer g-5+j (tiles 1, 2, 3 three, two and one
-  // layers ahead, tile 0 last), each after that layer's own tile, so the
-  // wait for a layer's tile never waits for them and no end of layer issues
-  // more than two tiles' worth of loads.
+  // Register prefetch: at the end of layer i (barrier C) the first four
+  // tiles of layer i+1 are issued. (Issuing a global layer's register tiles
+  // several layers ahead was measured slower: the waits of the layers in
+  // between then cover those loads too.)
   TileBuf buf[kPrefetchTiles];
-  LayerView cur, pend;
-  int32_t pend_layer = -1;  // global layer whose tiles are being issued early
-  int pend_next = 1;        // next early tile of pend_layer to issue
+  LayerView cur;
   auto prepare = [&](int32_t i) {  // at the end of layer i (i = -1: start)
     const int32_t n1 = i + 1;
     if (n1 >= p.layer_count) return;
-    const bool from_pend = n1 == pend_layer;
-    const LayerView v1 = from_pend ? pend : setup(n1, n1 & 1);
-    // A later global layer within reach of the early scheme?
-    int32_t g = -1;
-    for (int32_t l = n1 + 1; l < p.layer_count && l <= n1 + kPrefetchTiles - 1; ++l) {
-      if (is_global_i(l)) { g = l; break; }
-    }
-    const bool early = g >= 0 && !is_global_i(n1) && v1.n_tiles <= 1;
-    if (early && pend_layer != g) {
-      pend = setup(g, 2);
-      pend_layer = g;
-      pend_next = 1;
-    }
-    // Early tiles of g due by now: j <= kPrefetchTiles - (g - n1).
-    const int due = early ? kPrefetchTiles - (g - n1) : 0;
+    cur = setup(n1, n1 & 1);
 #pragma unroll
-    for (int j = 0; j < kPrefetchTiles; ++j) {
-      const bool for_pend = early && j >= pend_next && j <= due && j < pend.n_tiles;
-      const bool for_n1 = j < v1.n_tiles && (!from_pend || j == 0 || j >= pend_next);
-      if (for_pend) {
-        issue(buf[j], pend, j);
-      } else if (for_n1) {
-        issue(buf[j], v1, j);
-      }
-    }
-    if (early) pend_next = max(pend_next, due + 1);
-    if (from_pend) pend_layer = -1;
-    cur = v1;
+    for (int j = 0; j < kPrefetchTiles; ++j)
+      if (j < cur.n_tiles) issue(buf[j], cur, j);
   };
   prepare(-1);
 
