@@ -91,6 +91,8 @@ SIGNATURES = {
     "gemma4_runtime_set_host_seq_lengths": (_I32, [_P, _P, _I64]),
     "gemma4_runtime_device_ptr": (_P, [_P, _I32]),
     "gemma4_decode_split_plan": (_I32, [_CFG, _I32, _I32, _I32, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
+    "gemma4_decode_prep_append_bf16": (
+        _I32, [_P, _P, _P, _CFG, _P, _P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _P]),
     "gemma4_decode_step_workspace_bytes": (ctypes.c_size_t, [_I32]),
     "gemma4_decode_step_workspace_init": (_I32, [_P, ctypes.c_size_t, _I32, _P]),
     "gemma4_decode_step_status": (_I32, [_P, ctypes.POINTER(_I32)]),
@@ -247,6 +249,15 @@ def flash_attention_decode_combine_bf16(out, partial_m, partial_l, partial_acc,
     return lib().gemma4_flash_attention_decode_combine_bf16(
         ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(seq_lengths),
         config, split_size, num_splits, batch_count, stream_handle(stream))
+
+
+def decode_prep_append_bf16(q_prepared, cache_k, cache_v, config, page_table, token_position,
+                            layer, q, k, v, q_norm_weight, k_norm_weight, cos, sin,
+                            batch_count, stream=None) -> int:
+    return lib().gemma4_decode_prep_append_bf16(
+        ptr(q_prepared), ptr(cache_k), ptr(cache_v), config, ptr(page_table),
+        ptr(token_position), layer, ptr(q), ptr(k), ptr(v), ptr(q_norm_weight),
+        ptr(k_norm_weight), ptr(cos), ptr(sin), batch_count, stream_handle(stream))
 
 
 def decode_step_workspace_bytes(batch_count: int) -> int:

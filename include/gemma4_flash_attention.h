@@ -123,6 +123,24 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
                                     int32_t target_workgroups,
                                     int32_t *split_size, int32_t *num_splits);
 
+// Decode-token preparation + cache append (replaces
+// phase_decode_q_paged_kv_norm_rope, src/gemma4_flash_attention_decode.cu:285-375):
+// for each sequence b < batch_count with token_position[b] >= 0, every query
+// head of q [b][16][D] gets learned RMSNorm (q_norm_weight [D]) and split-half
+// RoPE over the rotary prefix (D for the (8,256) geometry, D/4 for (1,512)),
+// written to q_prepared [b][16][D]; each KV head's key [b][Hk][D] gets the
+// same with k_norm_weight and is stored in the cache row of token_position[b]
+// (its page's ring slot; skipped when the page is unmapped); V [b][Hk][D]
+// gets scale-free RMSNorm (for (1,512), V is the scale-free norm of the raw
+// key and `v` may be null). cos/sin: [position][rotary_dim/2] fp32 tables
+// (the runtime state's). eps 1e-6.
+hipError_t gemma4_decode_prep_append_bf16(
+    gemma4_bf16 *q_prepared, gemma4_bf16 *cache_k, gemma4_bf16 *cache_v,
+    Gemma4KvCacheConfig config, const int32_t *page_table, const int32_t *token_position,
+    int32_t layer, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    const gemma4_bf16 *q_norm_weight, const gemma4_bf16 *k_norm_weight, const float *cos,
+    const float *sin, int32_t batch_count, hipStream_t stream);
+
 // ---- persistent decode step over consecutive layers --------------------
 // One cooperative launch that runs, for model layers first_layer ..
 // first_layer + layer_count - 1 in order, the fused K/V append of the current
