@@ -296,12 +296,11 @@ def bench_batch64(torch, gk, dev, steps, warmup):
     pm = torch.empty(64 * QH * n, device=dev)
     pl = torch.empty_like(pm)
     pa = torch.empty(64 * QH * n * DIM, device=dev)
-    cnt = torch.zeros(64 * HEADS, dtype=torch.int32, device=dev)
 
-    def fn(st):
+    def fn(st):  # fused append + split kernel, then the combine kernel
         gk.check(gk.flash_attention_append_decode_paged_bf16(
             out, pm, pl, pa, q, ck, cv, pt, seq_t, pos_t, k, v, cfg, 0, 1 / 16, split, n, 64,
-            stream=st, split_counters=cnt), "batch64 decode")
+            stream=st, split_counters=None), "batch64 decode")
 
     ms, _ = time_graph(torch, fn, steps, warmup)
     total = sum(layer_bytes(int(s)) for s in seq)

@@ -307,8 +307,8 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
       t_.valid |= (row != kRowInvalid ? 1u : 0u) << kl;
       const bool fresh = row == kRowNewToken;
       const int64_t off = (int64_t)(row < 0 ? 0 : row) * Sh::kRowElems;
-      t_.k[kl] = load128(fresh ? p.new_k + new_off : kbase + off);
-      t_.v[kl] = load128(fresh ? p.new_v + new_off : vbase + off);
+      t_.k[kl] = load128_stream(fresh ? p.new_k + new_off : kbase + off);
+      t_.v[kl] = load128_stream(fresh ? p.new_v + new_off : vbase + off);
     }
   };
 
@@ -822,8 +822,11 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
   } else {
     return hipErrorInvalidValue;
   }
-  // Default: eight split workgroups per CU; ragged batches need the slack.
-  if (target_workgroups <= 0) target_workgroups = 2048;
+  // Default: eight split workgroups per CU for one sequence; a batch is
+  // sized by its longest sequence, so shorter ones leave workgroups idle:
+  // 32 per CU then (measured best on BASELINE config 3: 64 sequences, 512 to
+  // 32768 keys).
+  if (target_workgroups <= 0) target_workgroups = batch_count > 1 ? 8192 : 2048;
   const int64_t keys = (int64_t)std::max(max_live_keys, 1);
   const int64_t heads = (int64_t)batch_count * config.num_heads;
   int64_t splits_per_seq = (target_workgroups + heads - 1) / heads;

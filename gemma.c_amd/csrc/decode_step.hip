@@ -290,10 +290,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
 #pragma unroll
         for (int kl = 0; kl < kTileLoads; ++kl) {
           const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems;
+          // cache policy 2 = nontemporal: streamed once, keep L2 for the records
           __builtin_amdgcn_global_load_lds(kb + off, s_tiles + (filled * 8 + kl) * kWave, 16, 0,
-                                           0);
+                                           2);
           __builtin_amdgcn_global_load_lds(vb + off, s_tiles + (filled * 8 + 4 + kl) * kWave, 16,
-                                           0, 0);
+                                           0, 2);
         }
       }
     };
@@ -558,8 +559,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     for (int kl = 0; kl < kTileLoads; ++kl) {
       tb.valid |= (rows[kl] >= 0 ? 1u : 0u) << kl;
       const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems + col;
-      tb.k[kl] = load128(kb + off);
-      tb.v[kl] = load128(vb + off);
+      tb.k[kl] = load128_stream(kb + off);
+      tb.v[kl] = load128_stream(vb + off);
     }
   };
 

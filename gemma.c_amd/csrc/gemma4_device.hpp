@@ -34,6 +34,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ uint4 load128(const void *p) {
   return *reinterpret_cast<const uint4 *>(p);
 }
+// Streaming read of K/V data touched once per launch: the nontemporal hint
+// keeps it from displacing reused lines (flags, partials, tables) in L2.
+__device__ __forceinline__ uint4 load128_stream(const void *p) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 __device__ __forceinline__ void store128(void *p, uint4 v) {
   *reinterpret_cast<uint4 *>(p) = v;
 }
