@@ -191,6 +191,8 @@ struct LayerView {
   int32_t new_row;        // cache row this wave appends the new token to, or -1
   int32_t n_tiles;        // tiles of this wave
   bool owner;             // this wave attends over the new token
+  int32_t new_j;          // owner: wave-local tile of the new token (else -1)
+  int32_t new_r, new_kl;  // owner: its row half and load index in that tile
   bool lds;               // tiles 16 .. 16 + kLdsSlots - 1 of the split are in LDS
   int par;                // row table: s_rows[par]
 };
@@ -517,6 +519,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                                 ? append_row(c, p.page_table[kind], cache_layer, b, new_pos)
                                 : -1;
     v.owner = live_new && split == owner_split && wave == owner_wave;
+    {
+      const int32_t kk = new_pos - k0;  // key index of the new token in the split
+      v.new_j = v.owner ? (kk / kTileKeys) / kComputeWaves : -1;
+      v.new_r = (kk % kTileKeys) / kTileLoads;
+      v.new_kl = (kk % kTileKeys) % kTileLoads;
+    }
     v.lds = kind == 1;
     v.par = slot;
     v.kind = kind;
@@ -632,6 +640,28 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     scores(t.k, t.valid);
     accumulate(t.v, t.valid);
   };
+  // The appended token replaces its (masked) slot in its tile: the lanes of
+  // its row take the new K/V packs from LDS.
+  auto patch_packs = [&](uint4 (&x)[kTileLoads], uint32_t &valid, const LayerView &v,
+                         int half) __attribute__((always_inline)) {
+    const uint4 nw = s_new[half * kLPR + cpack];
+#pragma unroll
+    for (int kl = 0; kl < kTileLoads; ++kl) {
+      const bool sel = kl == v.new_kl && r == v.new_r;
+      x[kl].x = sel ? nw.x : x[kl].x;
+      x[kl].y = sel ? nw.y : x[kl].y;
+      x[kl].z = sel ? nw.z : x[kl].z;
+      x[kl].w = sel ? nw.w : x[kl].w;
+    }
+    valid |= r == v.new_r ? 1u << v.new_kl : 0u;
+  };
+  auto patch_tile = [&](TileBuf &t, const LayerView &v, int32_t j)
+                        __attribute__((always_inline)) {
+    if (v.owner && j == v.new_j) {
+      patch_packs(t.k, t.valid, v, 0);
+      patch_packs(t.v, t.valid, v, 1);
+    }
+  };
 
   // Register prefetch: at the end of layer i (barrier C) the first four
   // tiles of layer i+1 are issued. (Issuing a global layer's register tiles
@@ -680,7 +710,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       const int32_t n_stream = n > lds_end ? n - lds_end : 0;
 #pragma unroll
       for (int j = 0; j < kPrefetchTiles; ++j) {
-        if (j < n) compute(buf[j]);
+        if (j < n) {
+          patch_tile(buf[j], view, j);
+          compute(buf[j]);
+        }
         if (j < n_stream) issue(buf[j], view, lds_end + j);
       }
       for (int32_t j = kPrefetchTiles; j < lds_end; ++j) {
@@ -688,32 +721,29 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         const int4 rr = s_lds_rows[slot * 2 + r];
         const uint32_t valid = (rr.x >= 0 ? 1u : 0u) | (rr.y >= 0 ? 2u : 0u) |
                                (rr.z >= 0 ? 4u : 0u) | (rr.w >= 0 ? 8u : 0u);
+        uint32_t valid_k = valid, valid_v = valid;
+        const bool has_new = view.owner && j == view.new_j;
         uint4 kv[kTileLoads];
 #pragma unroll
         for (int kl = 0; kl < kTileLoads; ++kl) kv[kl] = s_tiles[(slot * 8 + kl) * kWave + lane];
-        scores(kv, valid);
+        if (has_new) patch_packs(kv, valid_k, view, 0);
+        scores(kv, valid_k);
 #pragma unroll
         for (int kl = 0; kl < kTileLoads; ++kl) kv[kl] = s_tiles[(slot * 8 + 4 + kl) * kWave + lane];
-        accumulate(kv, valid);
+        if (has_new) patch_packs(kv, valid_v, view, 1);
+        accumulate(kv, valid_v);
       }
       for (int32_t t0 = 0; t0 < n_stream; t0 += kPrefetchTiles) {
 #pragma unroll
         for (int j = 0; j < kPrefetchTiles; ++j) {
-          if (t0 + j < n_stream) compute(buf[j]);
+          if (t0 + j < n_stream) {
+            patch_tile(buf[j], view, lds_end + t0 + j);
+            compute(buf[j]);
+          }
           if (t0 + j + kPrefetchTiles < n_stream)
             issue(buf[j], view, lds_end + t0 + j + kPrefetchTiles);
         }
       }
-    }
-    if (view.owner) {
-      // The appended token: row 0 of a one-key tile, read from new K/V.
-      TileBuf nt;
-      const uint4 nk = s_new[cpack];
-      const uint4 nv = s_new[kLPR + cpack];
-#pragma unroll
-      for (int kl = 0; kl < kTileLoads; ++kl) { nt.k[kl] = nk; nt.v[kl] = nv; }
-      nt.valid = r == 0 ? 1u : 0u;
-      compute(nt);
     }
     if (view.new_row >= 0 && r == 0) {
       const int64_t dst = (int64_t)view.new_row * kRowElems + col;
