@@ -14,36 +14,61 @@
 //   * the online-softmax rescale is a per-lane scalar,
 //   * P^T feeds the second MFMA straight from registers (the contraction's
 //     key order is permuted to match, and V^T is read in that order).
-// Workgroup = (kv head, 64 chunk rows), 4 waves; wave w owns rows
-// [16w, 16w+16) for both GQA heads of the kv head (32 MFMA columns). K tiles
-// (32 keys) are staged row-major and V tiles transposed into LDS, double
-// buffered, with the next tile's global loads in flight during the current
-// tile's MFMAs. Blocks are ordered head-fastest so the workgroups of one kv
-// head land on one XCD and share its L2 as they stream the same keys.
+//
+// Workgroup = (kv head, 64 chunk rows), 4 waves, one per SIMD; wave w owns
+// rows [16w, 16w+16) for both GQA heads of the kv head (32 MFMA columns).
+// Keys stream in tiles of 64 through two LDS stages. Each tile's K and V rows
+// are copied into LDS by the waves themselves with global_load_lds (no
+// register staging): wave w copies keys [16w, 16w+16) of the tile, one 1 KiB
+// instruction per key pair, from addresses its lanes resolved through the
+// page table one tile earlier. The rows land XOR-swizzled in 16-byte chunks:
+//   * K row k, chunk c sits at chunk c ^ (k & 15): the 16 lanes of one
+//     ds_read_b128 pass read 16 keys at one logical chunk without bank
+//     conflicts;
+//   * V row k, chunk c sits at chunk c ^ ((k & 3) << 2): ds_read_b64_tr_b16
+//     hands lane i of a 16-lane group V[k0 + e][n0 + i] (e = 0..3) from four
+//     rows x 32 bytes, which this layout spreads over all banks. The
+//     transposing read turns row-major V into the V^T operand directly.
+// Tile t+1 is copied while tile t is computed; one barrier per tile.
+// Softmax maxima are updated lazily: the running max moves (and the
+// accumulators are rescaled) only when a row's new maximum exceeds it by
+// more than 8 in log2 units, so exp2 arguments stay <= 8 and the result is
+// unchanged up to rounding. Blocks of 32 keys that no row of a wave sees are
+// skipped, and blocks every row sees skip the mask. Blocks are ordered
+// head-fastest so the workgroups of one kv head land on one XCD and share its
+// L2 as they stream the same keys.
 #include "gemma4_device.hpp"
 
 #include "gemma4_flash_attention.h"
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace gemma4 {
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kPrefillThreads = 256;
-constexpr int kPrefillRows = 64;     // chunk rows per workgroup
-constexpr int kKeyTile = 32;         // keys per K/V tile
-constexpr int kKPad = 8;             // bf16 pad per K row (bank spread)
-constexpr int kVPad = 8;             // bf16 pad per V^T row
+constexpr int kPrefillWaves = kPrefillThreads / kWave;
+constexpr int kPrefillRows = 64;                 // chunk rows per workgroup
+constexpr int kDim = 256;                        // head_dim of the supported geometry
+constexpr int kRowBytes = kDim * 2;              // one bf16 K or V row of a head
+constexpr int kTileKeys = 64;                    // keys per LDS stage
+constexpr int kTileBytes = kTileKeys * kRowBytes;  // 32 KiB per stage and operand
+constexpr int kCopyKeys = kTileKeys / kPrefillWaves;  // keys each wave copies per tile
+constexpr float kRescaleSlack = 8.0f;           // log2 headroom of the lazy max
 
 struct PrefillParams {
   uint16_t *out;             // [B][Lq][16][D]
   const uint16_t *q;         // [B][Lq][16][D]
   const uint16_t *k;         // [B][Lq][Hk][D] chunk keys
   const uint16_t *v;
-  const uint16_t *cache_k;   // paged prior keys (may be null when no prior)
+  const uint16_t *cache_k;   // paged prior keys (null when no prior)
   const uint16_t *cache_v;
   const int32_t *page_table;
   const int32_t *prior;      // [B] keys already in the cache (null: 0)
@@ -59,20 +84,33 @@ __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-template <int D>
-struct PrefillSmem {
-  uint16_t k[2][kKeyTile][D + kKPad];
-  uint16_t vt[2][D][kKeyTile + kVPad];
-  alignas(16) int32_t valid[2][kKeyTile];
-};
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
 
-template <int D>
+// floor(n / d) for 0 <= n < 2^24 and d >= 1, from the fp32 reciprocal plus
+// one correction step each way.
+__device__ __forceinline__ int div_small(int n, int d, float inv_d) {
+  int q = (int)((float)n * inv_d);
+  q += (q + 1) * d <= n ? 1 : 0;
+  q -= q * d > n ? 1 : 0;
+  return q;
+}
+
+template <int kSt>
+using Stage = std::integral_constant<int, kSt>;
+
 __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(PrefillParams p) {
-  static_assert(D == 256, "tile shapes are sized for head_dim 256");
-  constexpr int KS = D / 16;        // k-steps of S^T (dims)
-  constexpr int DB = D / 32;        // 32-dim blocks of O^T
-  constexpr int KCH = kKeyTile * D / 8 / kPrefillThreads;  // 16-B K chunks per thread per tile
-  __shared__ PrefillSmem<D> sm;
+  constexpr int KS = kDim / 16;        // k-steps of S^T (dims)
+  constexpr int DB = kDim / 32;        // 32-dim blocks of O^T
+  __shared__ uint4 s_k0[kTileBytes / 16];
+  __shared__ uint4 s_k1[kTileBytes / 16];
+  __shared__ uint4 s_v0[kTileBytes / 16];
+  __shared__ uint4 s_v1[kTileBytes / 16];
+  __shared__ uint32_t s_valid[2][kPrefillWaves];      // bit j: key 16w + j of the stage is readable
+  __shared__ uint4 s_rows[kPrefillWaves][kCopyKeys];  // {K address, V address} per copied key
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -84,22 +122,29 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int q0 = (blockIdx.x / Hk) * kPrefillRows;
   const int b = blockIdx.y;
   const int Lq = p.chunk_len;
-  const int prior = p.prior != nullptr ? p.prior[b] : 0;
+  const int prior = p.prior != nullptr ? wave_uniform(p.prior[b]) : 0;
 
   // Rows of this lane: chunk row r = q0 + 16*wave + n % 16, q head 2*head + n / 16
   // (G = 2 for 16 query heads over 8 kv heads).
   const int G = kQueryHeads / Hk;
-  const int r_local = n % 16;
   const int g = n / 16;
-  const int row = q0 + 16 * wave + r_local;
+  const int row = q0 + 16 * wave + n % 16;
   const bool row_ok = row < Lq && g < G;
   const int qh = head * G + g;
   const int qpos = prior + row;  // absolute position of this query row
+  const int win_lo = p.window > 0 ? qpos - p.window : -1;  // visible: win_lo < kp <= qpos
+  // Wave-uniform row span for the block skip / no-mask tests.
+  const int wave_row0 = q0 + 16 * wave;
+  const bool wave_has_rows = wave_row0 < Lq;
+  const bool wave_rows_full = wave_row0 + 15 < Lq;
+  const int wave_qmin = prior + wave_row0;
+  const int wave_qmax = prior + min(wave_row0 + 15, Lq - 1);
 
   // Q^T operand: lane holds Q[row][16s + 8*half .. +8] for every k-step s.
   uint4 qreg[KS];
   {
-    const uint16_t *qrow = p.q + (((int64_t)b * Lq + (row_ok ? row : 0)) * kQueryHeads + qh) * D;
+    const uint16_t *qrow =
+        p.q + (((int64_t)b * Lq + (row_ok ? row : 0)) * kQueryHeads + qh) * kDim;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       qreg[s] = row_ok ? load128(qrow + 16 * s + 8 * half) : make_uint4(0, 0, 0, 0);
@@ -110,103 +155,109 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int wg_last = prior + min(q0 + kPrefillRows, Lq) - 1;  // last visible key of any row
   int kstart = p.window > 0 ? prior + q0 - p.window + 1 : 0;
   kstart = kstart < 0 ? 0 : kstart;
-  const int tile0 = (kstart / kKeyTile) * kKeyTile;
-  const int n_tiles = wg_last < tile0 ? 0 : (wg_last - tile0) / kKeyTile + 1;
+  const int tile0 = (kstart / kTileKeys) * kTileKeys;
+  const int n_tiles = (wg_last - tile0) / kTileKeys + 1;
 
-  // Staging assignment. K: thread t copies 16-B part (t % 32) of keys
-  // t/32 + 8i. V: thread t transposes keys 4*(t%8)..+3 x dims 8*(t/8)..+7.
-  // Thread-local key j (0..3 for K, 4..7 for V) of a tile at kt:
-  const int kpart = t % 32;
-  const int vkg = t % 8;
-  const int vdg = t / 8;
-  auto tile_key = [&](int j) { return j < 4 ? t / 32 + 8 * j : 4 * vkg + (j - 4); };
-
-  // Page lookups run two tiles ahead of the MFMAs: fetch_pages issues the
-  // page-table loads of a tile's prior keys; issue_tile turns them into
-  // source rows and issues the K/V loads of the next tile. Every load is
-  // unconditional (a harmless in-bounds word / dummy row when there is
-  // nothing to read) so no divergent branch disturbs the wait counters.
+  // ---- key rows: page lookup one tile ahead, addresses at copy time ------
+  // Lane j (= lane % 16) of wave w resolves key tile + 16w + j.
   const Gemma4KvCacheConfig &c = p.c;
   const bool paged = p.page_table != nullptr && prior > 0;
   const float inv_page = 1.0f / (float)c.page_size;
-  auto page_of = [&](int kp) {  // kp / page_size for 0 <= kp < 2^24
-    int lp = (int)((float)kp * inv_page);
-    lp += (lp + 1) * c.page_size <= kp ? 1 : 0;
-    lp -= lp * c.page_size > kp ? 1 : 0;
-    return lp;
-  };
-  const int32_t *pt_row = paged ? p.page_table + b * c.max_pages_per_seq
+  const float inv_pages = 1.0f / (float)c.max_pages_per_seq;
+  const int32_t *pt_row = paged ? p.page_table + (int64_t)b * c.max_pages_per_seq
                                 : reinterpret_cast<const int32_t *>(p.q);
-  const int pt_mod = paged ? c.max_pages_per_seq : 1;
-  auto fetch_pages = [&](int kt, int32_t (&pg)[8]) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int kp = kt + tile_key(j);
-      kp = kp < prior ? kp : prior - 1;  // chunk keys: any in-bounds slot
-      kp = kp < 0 ? 0 : kp;
-      pg[j] = pt_row[page_of(kp) % pt_mod];
+  const int key_lane = lane & (kCopyKeys - 1);
+  auto lookup_page = [&](int kt) __attribute__((always_inline)) -> int32_t {
+    int kp = kt + kCopyKeys * wave + key_lane;
+    kp = kp < prior ? kp : prior - 1;  // chunk keys: any in-bounds slot
+    kp = kp < 0 ? 0 : kp;
+    int slot = 0;
+    if (paged) {
+      const int lp = div_small(kp, c.page_size, inv_page);
+      slot = lp - div_small(lp, c.max_pages_per_seq, inv_pages) * c.max_pages_per_seq;
     }
+    return pt_row[slot];
   };
-  // Element offset of one key's row for this head, or -1 when the key is out
-  // of the workgroup's range or on an unmapped page; cache rows carry bit 62.
-  constexpr int64_t kCacheBit = 1ll << 62;
-  auto key_off = [&](int kp, int phys) -> int64_t {
-    const int64_t chunk_off = (((int64_t)b * Lq + (kp - prior)) * Hk + head) * D;
-    const int lp = page_of(kp < 0 ? 0 : kp);
-    const int64_t crow = ((int64_t)p.layer * c.num_pages + phys) * c.page_size + (kp - lp * c.page_size);
-    const int64_t cache_off = ((crow * Hk + head) * D) | kCacheBit;
-    const bool in_range = kp >= 0 && kp <= wg_last;
-    const bool cached_ok = paged && phys >= 0 && phys < c.num_pages;
-    const int64_t off = kp >= prior ? chunk_off : (cached_ok ? cache_off : -1);
-    return in_range ? off : -1;
-  };
-  auto src_of = [&](int64_t off, const uint16_t *cache, const uint16_t *chunk) {
-    const uint16_t *base = (off & kCacheBit) ? cache : chunk;
-    return off < 0 ? chunk : base + (off & ~kCacheBit);  // invalid: dummy row, masked later
+  const uint16_t *chunk_k = p.k, *chunk_v = p.v;
+  const int64_t layer_rows = (int64_t)p.layer * c.num_pages;
+  // Byte addresses of one key's K and V rows for this head, and whether the
+  // key can be read (in range, on a mapped page). Unreadable keys point at
+  // the first chunk row, which always exists, and are masked later.
+  auto resolve = [&](int kt, int32_t phys, uint4 &rows_out) __attribute__((always_inline)) -> bool {
+    const int kp = kt + kCopyKeys * wave + key_lane;
+    int64_t elem;
+    const uint16_t *kb;
+    const uint16_t *vb;
+    bool ok;
+    if (kp >= prior) {
+      ok = kp <= wg_last;
+      elem = (((int64_t)b * Lq + (ok ? kp - prior : 0)) * Hk + head) * kDim;
+      kb = chunk_k;
+      vb = chunk_v;
+    } else {
+      const int lp = div_small(kp, c.page_size, inv_page);
+      ok = paged && phys >= 0 && phys < c.num_pages;
+      const int64_t crow = (layer_rows + phys) * c.page_size + (kp - lp * c.page_size);
+      elem = (crow * Hk + head) * kDim;
+      kb = ok ? p.cache_k : chunk_k;
+      vb = ok ? p.cache_v : chunk_v;
+      if (!ok) elem = ((int64_t)b * Lq * Hk + head) * kDim;
+    }
+    const uint64_t ka = reinterpret_cast<uint64_t>(kb + elem);
+    const uint64_t va = reinterpret_cast<uint64_t>(vb + elem);
+    rows_out = make_uint4((uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32));
+    return ok;
   };
 
-  struct Stage {
-    uint4 k[KCH];
-    uint4 v[4];
-    uint32_t valid;  // bit i: K key t/32 + 8i valid; bit 4+i: V key 4*(t%8)+i valid
-  };
-  auto issue_tile = [&](Stage &st, int kt, const int32_t (&pg)[8]) {
-    st.valid = 0;
+  // Source chunk of each copy lane: instruction a of a wave copies keys
+  // 16w + 2a (lanes 0..31) and 16w + 2a + 1 (lanes 32..63); lane l fills
+  // LDS chunk l % 32 of its key with the swizzled source chunk.
+  int src_k[kCopyKeys / 2], src_v[kCopyKeys / 2];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int64_t off = key_off(kt + tile_key(i), pg[i]);
-      st.valid |= (off >= 0 ? 1u : 0u) << i;
-      st.k[i] = load128(src_of(off, p.cache_k, p.k) + kpart * 8);
-    }
+  for (int a = 0; a < kCopyKeys / 2; ++a) {
+    const int key = 2 * a + half;  // key index mod 16 (16w is a multiple of 16)
+    src_k[a] = (n ^ (key & 15)) * 16;
+    src_v[a] = (n ^ ((key & 3) << 2)) * 16;
+  }
+
+  auto copy_tile = [&](auto st, int kt, int32_t phys) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+    uint4 *dk = S == 0 ? s_k0 : s_k1;
+    uint4 *dv = S == 0 ? s_v0 : s_v1;
+    uint4 rows;
+    const bool ok = resolve(kt, phys, rows);
+    const uint32_t ok_bits = (uint32_t)__builtin_amdgcn_ballot_w64(ok) & 0xFFFFu;
+    if (lane < kCopyKeys) s_rows[wave][lane] = rows;
+    if (lane == 0) s_valid[S][wave] = ok_bits;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t off = key_off(kt + tile_key(4 + i), pg[4 + i]);
-      st.valid |= (off >= 0 ? 1u : 0u) << (4 + i);
-      st.v[i] = load128(src_of(off, p.cache_v, p.v) + vdg * 8);
-    }
-  };
-  auto store_tile = [&](const Stage &st, int buf) {
-#pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const bool ok = (st.valid >> i) & 1u;
-      store128(&sm.k[buf][t / 32 + 8 * i][kpart * 8], ok ? st.k[i] : make_uint4(0, 0, 0, 0));
-      if (kpart == 0) sm.valid[buf][t / 32 + 8 * i] = ok ? 1 : 0;
-    }
-    uint32_t w[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 vv = ((st.valid >> (4 + i)) & 1u) ? st.v[i] : make_uint4(0, 0, 0, 0);
-      w[i][0] = vv.x; w[i][1] = vv.y; w[i][2] = vv.z; w[i][3] = vv.w;
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-      uint2 pair;
-      pair.x = __builtin_amdgcn_perm(w[1][e / 2], w[0][e / 2], sel);
-      pair.y = __builtin_amdgcn_perm(w[3][e / 2], w[2][e / 2], sel);
-      *reinterpret_cast<uint2 *>(&sm.vt[buf][vdg * 8 + e][4 * vkg]) = pair;
+    for (int a = 0; a < kCopyKeys / 2; ++a) {
+      const uint4 r = s_rows[wave][2 * a + half];
+      const uint64_t ka = ((uint64_t)r.y << 32) | r.x;
+      const uint64_t va = ((uint64_t)r.w << 32) | r.z;
+      const int dst = (kCopyKeys * wave + 2 * a) * (kRowBytes / 16);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(ka + src_k[a]), dk + dst,
+                                       16, 0, 0);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(va + src_v[a]), dv + dst,
+                                       16, 0, 0);
     }
   };
+
+  // ---- LDS read offsets (bytes within a stage) ----------------------------
+  // K operand of S^T k-step s: key 32*blk + n, logical chunk 2s + half.
+  int koff[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) koff[s] = n * kRowBytes + (((2 * s + half) ^ (n & 15)) << 4);
+  // V^T operand of dim block d: lane i of 16-lane group gsel reads key
+  // k0 + j, dims 32d + 16 gsel + 4q (j = (lane % 16) / 4, q = lane % 4),
+  // k0 = 32*blk + 16*s2 + 8*r + 4*half.
+  const int vj = (lane & 15) >> 2;
+  const int vq = lane & 3;
+  const int vg = (lane >> 4) & 1;
+  int voff[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d)
+    voff[d] = (4 * half + vj) * kRowBytes + (((4 * (d ^ vj) + 2 * vg + (vq >> 1)) << 4) |
+                                             ((vq & 1) << 3));
 
   // Online softmax state: lane's row; lanes l and l^32 share a row.
   float m_run = -INFINITY;
@@ -215,96 +266,119 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
 #pragma unroll
   for (int d = 0; d < DB; ++d) acc[d] = f32x16_t{};
 
-  Stage st;
-  int32_t pages[8];
-  if (n_tiles > 0) {
-    fetch_pages(tile0, pages);
-    issue_tile(st, tile0, pages);
-    fetch_pages(tile0 + kKeyTile, pages);
-    store_tile(st, 0);
-  }
-  __syncthreads();
-
-  for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
-    const int kt = tile0 + it * kKeyTile;
-    const bool more = it + 1 < n_tiles;
-    if (more) {
-      issue_tile(st, kt + kKeyTile, pages);              // in flight during the MFMAs
-      fetch_pages(kt + 2 * kKeyTile, pages);             // two tiles ahead
-    }
-
+  // One block of 32 keys: S^T, masked softmax, O^T += V^T P^T.
+  auto attend_block = [&](const char *kbase, const char *vbase, int kb_lo, uint32_t valid32) __attribute__((always_inline)) {
+    const int kb_hi = kb_lo + 31;
+    if (!wave_has_rows || kb_lo > wave_qmax) return;
+    if (p.window > 0 && kb_hi <= wave_qmin - p.window) return;
+    const bool full = wave_rows_full && valid32 == 0xFFFFFFFFu && kb_hi <= wave_qmin &&
+                      (p.window == 0 || kb_lo > wave_qmax - p.window);
     // S^T[key m][row n] = sum_d K[m][d] Q[n][d], as two independent chains.
     f32x16_t s_even = f32x16_t{}, s_odd = f32x16_t{};
 #pragma unroll
     for (int s = 0; s < KS; s += 2) {
-      const uint4 k0 = *reinterpret_cast<const uint4 *>(&sm.k[buf][n][16 * s + 8 * half]);
-      const uint4 k1 = *reinterpret_cast<const uint4 *>(&sm.k[buf][n][16 * s + 16 + 8 * half]);
+      const uint4 k0 = *reinterpret_cast<const uint4 *>(kbase + koff[s]);
+      const uint4 k1 = *reinterpret_cast<const uint4 *>(kbase + koff[s + 1]);
       s_even = mfma32(k0, qreg[s], s_even);
       s_odd = mfma32(k1, qreg[s + 1], s_odd);
     }
     const f32x16_t s_acc = s_even + s_odd;
     // Lane holds keys m = (i/4)*8 + 4*half + i%4, i = 0..15, of row n.
-    int flags[16];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int4 f = *reinterpret_cast<const int4 *>(&sm.valid[buf][8 * j + 4 * half]);
-      flags[4 * j] = f.x; flags[4 * j + 1] = f.y; flags[4 * j + 2] = f.z; flags[4 * j + 3] = f.w;
-    }
-    const int win_lo = p.window > 0 ? qpos - p.window : -1;  // visible: win_lo < kp <= qpos
     float sc[16];
     float tmax = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kp = kt + (i / 4) * 8 + 4 * half + (i % 4);
-      const bool vis = row_ok & (flags[i] != 0) & (kp <= qpos) & (kp > win_lo);
-      sc[i] = vis ? s_acc[i] * p.q_scale : -INFINITY;
-      tmax = fmaxf(tmax, sc[i]);
+      for (int i = 0; i < 16; ++i) {
+        sc[i] = s_acc[i] * p.q_scale;
+        tmax = fmaxf(tmax, sc[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = (i / 4) * 8 + 4 * half + (i % 4);
+        const int kp = kb_lo + m;
+        const bool vis = row_ok & (((valid32 >> m) & 1u) != 0) & (kp <= qpos) & (kp > win_lo);
+        sc[i] = vis ? s_acc[i] * p.q_scale : -INFINITY;
+        tmax = fmaxf(tmax, sc[i]);
+      }
     }
     tmax = fmaxf(tmax, lane_xor<32>(tmax));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    // Rescale only when some row's maximum moved (exactly; alpha == 1 else).
-    if (__builtin_amdgcn_ballot_w64(m_new > m_run) != 0) {
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    // Lazy maximum: move it (and rescale) only when a row outgrew it by more
+    // than the slack; otherwise exp2 arguments stay below the slack.
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kRescaleSlack) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
       for (int d = 0; d < DB; ++d) acc[d] *= alpha;
+      m_run = m_new;
     }
-    m_run = m_new;
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
     uint32_t pw[8];
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       const float p0 = __builtin_amdgcn_exp2f(sc[i] - m_use);
       const float p1 = __builtin_amdgcn_exp2f(sc[i + 1] - m_use);
       l_run += p0 + p1;
-      pw[i / 2] = pack_bf16x2(p0, p1);
+      pw[i / 2] = cvt_pk_bf16(p0, p1);
     }
     // O^T[dim][row] += sum over keys V^T[dim][key] P^T[key][row]; k-step s2
-    // covers keys 16*s2 + {4h..4h+3, 8+4h..8+4h+3} for lane half h.
+    // covers keys 16*s2 + {4h..4h+3, 8+4h..8+4h+3} for lane half h, the two
+    // groups of four read by one transposing load each.
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       const uint4 pb = make_uint4(pw[4 * s2], pw[4 * s2 + 1], pw[4 * s2 + 2], pw[4 * s2 + 3]);
-      uint4 vf[DB];  // all fragments of this k-step first: one LDS wait, then DB MFMAs
+      uint4 vf[DB];
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
-        const uint16_t *vrow = &sm.vt[buf][32 * d + n][16 * s2 + 4 * half];
-        const uint2 lo = *reinterpret_cast<const uint2 *>(vrow);
-        const uint2 hi = *reinterpret_cast<const uint2 *>(vrow + 8);
-        vf[d] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+        const char *base = vbase + (16 * s2) * kRowBytes + voff[d];
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4 *)(__attribute__((address_space(3))) char *)(base));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4 *)(__attribute__((address_space(3))) char *)(base + 8 * kRowBytes));
+        const uint2 l2 = __builtin_bit_cast(uint2, lo);
+        const uint2 h2 = __builtin_bit_cast(uint2, hi);
+        vf[d] = make_uint4(l2.x, l2.y, h2.x, h2.y);
       }
 #pragma unroll
       for (int d = 0; d < DB; ++d) acc[d] = mfma32(vf[d], pb, acc[d]);
     }
-    if (more) store_tile(st, buf ^ 1);
-    __syncthreads();
+  };
+
+  auto compute_tile = [&](auto st, int kt) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+    const char *kbase = reinterpret_cast<const char *>(S == 0 ? s_k0 : s_k1);
+    const char *vbase = reinterpret_cast<const char *>(S == 0 ? s_v0 : s_v1);
+    const uint4 vw = *reinterpret_cast<const uint4 *>(&s_valid[S][0]);
+    attend_block(kbase, vbase, kt, vw.x | (vw.y << 16));
+    attend_block(kbase + 32 * kRowBytes, vbase + 32 * kRowBytes, kt + 32, vw.z | (vw.w << 16));
+  };
+
+  // ---- pipeline: copy tile i+1 and look up tile i+2 while computing i -----
+  int32_t phys = lookup_page(tile0);
+  copy_tile(Stage<0>{}, tile0, phys);
+  if (n_tiles > 1) phys = lookup_page(tile0 + kTileKeys);
+  auto step = [&](auto st, int it) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+    const int kt = tile0 + it * kTileKeys;
+    __syncthreads();  // tile it copied (each wave waited for its own copies); stage S^1 free
+    if (it + 1 < n_tiles) {
+      copy_tile(Stage<S ^ 1>{}, kt + kTileKeys, phys);
+      if (it + 2 < n_tiles) phys = lookup_page(kt + 2 * kTileKeys);
+    }
+    compute_tile(st, kt);
+  };
+  for (int it = 0; it < n_tiles; it += 2) {
+    step(Stage<0>{}, it);
+    if (it + 1 < n_tiles) step(Stage<1>{}, it + 1);
   }
 
   // Normalise and store: lane holds dims 32d + (i/4)*8 + 4*half + i%4 of row n.
   l_run += lane_xor<32>(l_run);
   if (!row_ok) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  uint16_t *orow = p.out + (((int64_t)b * Lq + row) * kQueryHeads + qh) * D;
+  uint16_t *orow = p.out + (((int64_t)b * Lq + row) * kQueryHeads + qh) * kDim;
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -332,7 +406,7 @@ extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
   const bool paged = d_prior_lengths != nullptr;
   if (batch_size < 0 || chunk_len < 0 || batch_size > 65535 || !(softmax_scale > 0.0f) ||
       d_out == nullptr || d_q == nullptr || d_k == nullptr || d_v == nullptr ||
-      config.num_heads != 8 || config.head_dim != 256 || config.window_size < 0) {
+      config.num_heads != 8 || config.head_dim != kDim || config.window_size < 0) {
     return hipErrorInvalidValue;
   }
   if (paged && (d_cache_k == nullptr || d_cache_v == nullptr || d_page_table == nullptr ||
@@ -351,12 +425,17 @@ extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
   p.page_table = paged ? d_page_table : nullptr;
   p.prior = d_prior_lengths;
   p.c = config;
-  p.layer = layer;
+  if (!paged) {
+    // Without a prior context no page is read; keep the divisors valid.
+    p.c.page_size = 1;
+    p.c.max_pages_per_seq = 1;
+  }
+  p.layer = paged ? layer : 0;
   p.chunk_len = chunk_len;
   p.window = config.window_size;
   p.q_scale = softmax_scale * kLog2e;
   const int blocks = config.num_heads * ((chunk_len + kPrefillRows - 1) / kPrefillRows);
-  hipLaunchKernelGGL(prefill_chunk_kernel<256>, dim3(blocks, batch_size),
-                     dim3(kPrefillThreads), 0, stream, p);
+  hipLaunchKernelGGL(prefill_chunk_kernel, dim3(blocks, batch_size), dim3(kPrefillThreads), 0,
+                     stream, p);
   return hipGetLastError();
 }
