@@ -99,14 +99,108 @@ __device__ __forceinline__ int div_small(int n, int d, float inv_d) {
   return q;
 }
 
+typedef unsigned u32x4v_t __attribute__((ext_vector_type(4)));
+
+// Issues the 16 K-fragment reads of one S^T block (32 keys x 256 dims) so
+// that all are in flight before the first MFMA; the fragments land in AGPRs.
+// k_addr is the LDS byte address of k-step 0 for this lane; k-step s sits at
+// k_addr ^ (s << 5) (the XOR swizzle of the K rows, see the kernel comment),
+// plus kImm for the stage and block. The reads are invisible to the
+// compiler's counters: fragment s is consumed only after kfrag_ready(s).
+template <int kImm>
+__device__ __forceinline__ void read_kfrags(uint32_t k_addr, u32x4v_t (&kf)[16]) {
+  uint32_t t0, t1;
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "v_xor_b32 %[t0], 0, %[ka]\n\t"
+      "ds_read_b128 %[f0], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 32, %[ka]\n\t"
+      "ds_read_b128 %[f1], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 64, %[ka]\n\t"
+      "ds_read_b128 %[f2], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 96, %[ka]\n\t"
+      "ds_read_b128 %[f3], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 128, %[ka]\n\t"
+      "ds_read_b128 %[f4], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 160, %[ka]\n\t"
+      "ds_read_b128 %[f5], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 192, %[ka]\n\t"
+      "ds_read_b128 %[f6], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 224, %[ka]\n\t"
+      "ds_read_b128 %[f7], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 256, %[ka]\n\t"
+      "ds_read_b128 %[f8], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 288, %[ka]\n\t"
+      "ds_read_b128 %[f9], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 320, %[ka]\n\t"
+      "ds_read_b128 %[f10], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 352, %[ka]\n\t"
+      "ds_read_b128 %[f11], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 384, %[ka]\n\t"
+      "ds_read_b128 %[f12], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 416, %[ka]\n\t"
+      "ds_read_b128 %[f13], %[t1] offset:%[imm]\n\t"
+      "v_xor_b32 %[t0], 448, %[ka]\n\t"
+      "ds_read_b128 %[f14], %[t0] offset:%[imm]\n\t"
+      "v_xor_b32 %[t1], 480, %[ka]\n\t"
+      "ds_read_b128 %[f15], %[t1] offset:%[imm]"
+      : [t0] "=&v"(t0), [t1] "=&v"(t1),
+        [f0] "=&a"(kf[0]), [f1] "=&a"(kf[1]), [f2] "=&a"(kf[2]), [f3] "=&a"(kf[3]), [f4]
+        "=&a"(kf[4]), [f5] "=&a"(kf[5]), [f6] "=&a"(kf[6]), [f7] "=&a"(kf[7]), [f8]
+        "=&a"(kf[8]), [f9] "=&a"(kf[9]), [f10] "=&a"(kf[10]), [f11] "=&a"(kf[11]), [f12]
+        "=&a"(kf[12]), [f13] "=&a"(kf[13]), [f14] "=&a"(kf[14]), [f15] "=&a"(kf[15])
+      : [ka] "v"(k_addr), [imm] "i"(kImm));
+}
+
+// Waits until fragment kStep of read_kfrags has landed (LDS returns in
+// order, so at most 15 - kStep of the block's reads may still be pending;
+// any other LDS or scalar load in flight only makes the wait stricter).
+template <int kStep>
+__device__ __forceinline__ void kfrag_ready(u32x4v_t &f) {
+  asm volatile("s_waitcnt lgkmcnt(%[n])" : "+a"(f) : [n] "i"(15 - kStep));
+}
+
+// One 1 KiB LDS copy (global_load_lds, 16 bytes per lane): LDS bytes
+// [lds_addr, +1024) from the per-lane addresses src. The copy is invisible
+// to the compiler's memory counters: the caller waits for it (vmcnt) before
+// the barrier that publishes the tile.
+__device__ __forceinline__ void copy_row_pair(uint64_t src, uint32_t lds_addr) {
+  uint32_t m0_saved;
+  asm volatile(
+      "s_mov_b32 %[m0s], m0\n\t"
+      "s_mov_b32 m0, %[lds]\n\t"
+      "global_load_lds_dwordx4 %[src], off\n\t"
+      "s_mov_b32 m0, %[m0s]"
+      : [m0s] "=&s"(m0_saved)
+      : [lds] "s"(lds_addr), [src] "v"(src));
+}
+
+// Waits for every vector memory operation of this wave, the copies
+// included (s_waitcnt vmcnt(0); a builtin rather than inline asm so the
+// compiler's own counter bookkeeping sees it as well).
+__device__ __forceinline__ void wait_copies() {
+  constexpr int kVmcnt0 = 0x0F70;  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15 (no wait)
+  __builtin_amdgcn_s_waitcnt(kVmcnt0);
+}
+
+// f(integral_constant<int, I>) for I = kBegin .. kEnd-1, unrolled.
+template <int kBegin, int kEnd, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (kBegin < kEnd) {
+    f(std::integral_constant<int, kBegin>{});
+    static_for<kBegin + 1, kEnd>(f);
+  }
+}
+
 template <int kSt>
 using Stage = std::integral_constant<int, kSt>;
 
 __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(PrefillParams p) {
   constexpr int KS = kDim / 16;        // k-steps of S^T (dims)
   constexpr int DB = kDim / 32;        // 32-dim blocks of O^T
-  __shared__ uint4 s_k0[kTileBytes / 16];
-  __shared__ uint4 s_k1[kTileBytes / 16];
+  // K stages are read only by score_block (inline asm), so one array holds
+  // both; 512-byte alignment keeps the XOR swizzle out of the base address.
+  __shared__ __attribute__((aligned(1024))) uint4 s_k[2][kTileBytes / 16];
   __shared__ uint4 s_v0[kTileBytes / 16];
   __shared__ uint4 s_v1[kTileBytes / 16];
   __shared__ uint32_t s_valid[2][kPrefillWaves];      // bit j: key 16w + j of the stage is readable
@@ -141,13 +235,14 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int wave_qmax = prior + min(wave_row0 + 15, Lq - 1);
 
   // Q^T operand: lane holds Q[row][16s + 8*half .. +8] for every k-step s.
-  uint4 qreg[KS];
+  u32x4v_t qreg[KS];
   {
     const uint16_t *qrow =
         p.q + (((int64_t)b * Lq + (row_ok ? row : 0)) * kQueryHeads + qh) * kDim;
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      qreg[s] = row_ok ? load128(qrow + 16 * s + 8 * half) : make_uint4(0, 0, 0, 0);
+      const uint4 x = row_ok ? load128(qrow + 16 * s + 8 * half) : make_uint4(0, 0, 0, 0);
+      qreg[s] = u32x4v_t{x.x, x.y, x.z, x.w};
     }
   }
 
@@ -212,41 +307,49 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   // Source chunk of each copy lane: instruction a of a wave copies keys
   // 16w + 2a (lanes 0..31) and 16w + 2a + 1 (lanes 32..63); lane l fills
   // LDS chunk l % 32 of its key with the swizzled source chunk.
-  int src_k[kCopyKeys / 2], src_v[kCopyKeys / 2];
-#pragma unroll
-  for (int a = 0; a < kCopyKeys / 2; ++a) {
-    const int key = 2 * a + half;  // key index mod 16 (16w is a multiple of 16)
-    src_k[a] = (n ^ (key & 15)) * 16;
-    src_v[a] = (n ^ ((key & 3) << 2)) * 16;
-  }
+  auto src_k = [&](int a) __attribute__((always_inline)) {
+    return (n ^ ((2 * a + half) & 15)) * 16;  // key index mod 16 (16w is a multiple of 16)
+  };
+  auto src_v = [&](int a) __attribute__((always_inline)) {
+    return (n ^ (((2 * a + half) & 3) << 2)) * 16;
+  };
 
-  auto copy_tile = [&](auto st, int kt, int32_t phys) __attribute__((always_inline)) {
+  // Row addresses of the next tile: lane j < 16 resolves key 16w + j and
+  // publishes {K row, V row} in the wave's row table and the stage's validity
+  // bits; lane l then fetches key 16w + 2a + l/32 of copy a and adds its
+  // swizzled source chunk.
+  auto prepare_copy = [&](auto st, int kt, int32_t phys, uint64_t (&ksrc)[kCopyKeys / 2],
+                          uint64_t (&vsrc)[kCopyKeys / 2]) __attribute__((always_inline)) {
     constexpr int S = decltype(st)::value;
-    uint4 *dk = S == 0 ? s_k0 : s_k1;
-    uint4 *dv = S == 0 ? s_v0 : s_v1;
     uint4 rows;
     const bool ok = resolve(kt, phys, rows);
     const uint32_t ok_bits = (uint32_t)__builtin_amdgcn_ballot_w64(ok) & 0xFFFFu;
     if (lane < kCopyKeys) s_rows[wave][lane] = rows;
     if (lane == 0) s_valid[S][wave] = ok_bits;
+    uint4 rr[kCopyKeys / 2];
+#pragma unroll
+    for (int a = 0; a < kCopyKeys / 2; ++a) rr[a] = s_rows[wave][2 * a + half];
 #pragma unroll
     for (int a = 0; a < kCopyKeys / 2; ++a) {
-      const uint4 r = s_rows[wave][2 * a + half];
-      const uint64_t ka = ((uint64_t)r.y << 32) | r.x;
-      const uint64_t va = ((uint64_t)r.w << 32) | r.z;
-      const int dst = (kCopyKeys * wave + 2 * a) * (kRowBytes / 16);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(ka + src_k[a]), dk + dst,
-                                       16, 0, 0);
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void *>(va + src_v[a]), dv + dst,
-                                       16, 0, 0);
+      ksrc[a] = (((uint64_t)rr[a].y << 32) | rr[a].x) + src_k(a);
+      vsrc[a] = (((uint64_t)rr[a].w << 32) | rr[a].z) + src_v(a);
     }
   };
+  // LDS byte address of this wave's copy destination in each stage.
+  auto lds_addr = [](const void *ptr) __attribute__((always_inline)) -> uint32_t {
+    return (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char *)ptr);
+  };
+  const int copy_row0 = kCopyKeys * wave * (kRowBytes / 16);
+  const uint32_t k_dst[2] = {(uint32_t)wave_uniform(lds_addr(&s_k[0][copy_row0])),
+                             (uint32_t)wave_uniform(lds_addr(&s_k[1][copy_row0]))};
+  const uint32_t v_dst[2] = {(uint32_t)wave_uniform(lds_addr(&s_v0[copy_row0])),
+                             (uint32_t)wave_uniform(lds_addr(&s_v1[copy_row0]))};
 
   // ---- LDS read offsets (bytes within a stage) ----------------------------
   // K operand of S^T k-step s: key 32*blk + n, logical chunk 2s + half.
-  int koff[KS];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) koff[s] = n * kRowBytes + (((2 * s + half) ^ (n & 15)) << 4);
+  const uint32_t k_addr =
+      (uint32_t)reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) uint4 *)&s_k[0][0]) +
+      n * kRowBytes + ((half ^ (n & 15)) << 4);
   // V^T operand of dim block d: lane i of 16-lane group gsel reads key
   // k0 + j, dims 32d + 16 gsel + 4q (j = (lane % 16) / 4, q = lane % 4),
   // k0 = 32*blk + 16*s2 + 8*r + 4*half.
@@ -267,22 +370,34 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   for (int d = 0; d < DB; ++d) acc[d] = f32x16_t{};
 
   // One block of 32 keys: S^T, masked softmax, O^T += V^T P^T.
-  auto attend_block = [&](const char *kbase, const char *vbase, int kb_lo, uint32_t valid32) __attribute__((always_inline)) {
+  // The copy of the next tile rides on the block's score MFMAs (issued
+  // even when the block itself is skipped).
+  auto attend_block = [&](auto kimm, const char *vbase, int kb_lo, uint32_t valid32, bool copy,
+                          const uint64_t (&src)[kCopyKeys / 2], uint32_t dst) __attribute__((always_inline)) {
     const int kb_hi = kb_lo + 31;
-    if (!wave_has_rows || kb_lo > wave_qmax) return;
-    if (p.window > 0 && kb_hi <= wave_qmin - p.window) return;
+    if (!wave_has_rows || kb_lo > wave_qmax || (p.window > 0 && kb_hi <= wave_qmin - p.window)) {
+      if (copy) {
+#pragma unroll
+        for (int c = 0; c < kCopyKeys / 2; ++c) copy_row_pair(src[c], dst + c * 2 * kRowBytes);
+      }
+      return;
+    }
     const bool full = wave_rows_full && valid32 == 0xFFFFFFFFu && kb_hi <= wave_qmin &&
                       (p.window == 0 || kb_lo > wave_qmax - p.window);
-    // S^T[key m][row n] = sum_d K[m][d] Q[n][d], as two independent chains.
-    f32x16_t s_even = f32x16_t{}, s_odd = f32x16_t{};
-#pragma unroll
-    for (int s = 0; s < KS; s += 2) {
-      const uint4 k0 = *reinterpret_cast<const uint4 *>(kbase + koff[s]);
-      const uint4 k1 = *reinterpret_cast<const uint4 *>(kbase + koff[s + 1]);
-      s_even = mfma32(k0, qreg[s], s_even);
-      s_odd = mfma32(k1, qreg[s + 1], s_odd);
-    }
-    const f32x16_t s_acc = s_even + s_odd;
+    // S^T[key m][row n] = sum_d K[m][d] Q[n][d].
+    u32x4v_t kf[KS];
+    read_kfrags<decltype(kimm)::value>(k_addr, kf);
+    f32x16_t s_acc = f32x16_t{};
+    // The next tile's copies ride between the first eight MFMAs.
+    auto step_s = [&](auto sc) __attribute__((always_inline)) {
+      constexpr int s = decltype(sc)::value;
+      kfrag_ready<s>(kf[s]);
+      s_acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s]),
+                                                      __builtin_bit_cast(bf16x8_t, qreg[s]), s_acc,
+                                                      0, 0, 0);
+      if (s < kCopyKeys / 2 && copy) copy_row_pair(src[s % 8], dst + (s % 8) * 2 * kRowBytes);
+    };
+    static_for<0, KS>(step_s);
     // Lane holds keys m = (i/4)*8 + 4*half + i%4, i = 0..15, of row n.
     float sc[16];
     float tmax = -INFINITY;
@@ -346,28 +461,40 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     }
   };
 
-  auto compute_tile = [&](auto st, int kt) __attribute__((always_inline)) {
+  auto compute_tile = [&](auto st, int kt, bool copy, const uint64_t (&ksrc)[kCopyKeys / 2],
+                          const uint64_t (&vsrc)[kCopyKeys / 2]) __attribute__((always_inline)) {
     constexpr int S = decltype(st)::value;
-    const char *kbase = reinterpret_cast<const char *>(S == 0 ? s_k0 : s_k1);
     const char *vbase = reinterpret_cast<const char *>(S == 0 ? s_v0 : s_v1);
     const uint4 vw = *reinterpret_cast<const uint4 *>(&s_valid[S][0]);
-    attend_block(kbase, vbase, kt, vw.x | (vw.y << 16));
-    attend_block(kbase + 32 * kRowBytes, vbase + 32 * kRowBytes, kt + 32, vw.z | (vw.w << 16));
+    attend_block(std::integral_constant<int, S * kTileBytes>{}, vbase, kt, vw.x | (vw.y << 16),
+                 copy, ksrc, k_dst[S ^ 1]);
+    attend_block(std::integral_constant<int, S * kTileBytes + 32 * kRowBytes>{},
+                 vbase + 32 * kRowBytes, kt + 32, vw.z | (vw.w << 16), copy, vsrc, v_dst[S ^ 1]);
   };
 
   // ---- pipeline: copy tile i+1 and look up tile i+2 while computing i -----
+  uint64_t ksrc[kCopyKeys / 2], vsrc[kCopyKeys / 2];
   int32_t phys = lookup_page(tile0);
-  copy_tile(Stage<0>{}, tile0, phys);
+  prepare_copy(Stage<0>{}, tile0, phys, ksrc, vsrc);
+#pragma unroll
+  for (int c = 0; c < kCopyKeys / 2; ++c) {
+    copy_row_pair(ksrc[c], k_dst[0] + c * 2 * kRowBytes);
+    copy_row_pair(vsrc[c], v_dst[0] + c * 2 * kRowBytes);
+  }
   if (n_tiles > 1) phys = lookup_page(tile0 + kTileKeys);
   auto step = [&](auto st, int it) __attribute__((always_inline)) {
     constexpr int S = decltype(st)::value;
     const int kt = tile0 + it * kTileKeys;
-    __syncthreads();  // tile it copied (each wave waited for its own copies); stage S^1 free
-    if (it + 1 < n_tiles) {
-      copy_tile(Stage<S ^ 1>{}, kt + kTileKeys, phys);
+    // Tile it copied: each wave waits for its own copies, the barrier for all.
+    // Every wave has also finished tile it-1, so stage S^1 is free.
+    wait_copies();
+    __syncthreads();
+    const bool copy = it + 1 < n_tiles;
+    if (copy) {
+      prepare_copy(Stage<S ^ 1>{}, kt + kTileKeys, phys, ksrc, vsrc);
       if (it + 2 < n_tiles) phys = lookup_page(kt + 2 * kTileKeys);
     }
-    compute_tile(st, kt);
+    compute_tile(st, kt, copy, ksrc, vsrc);
   };
   for (int it = 0; it < n_tiles; it += 2) {
     step(Stage<0>{}, it);

@@ -31,6 +31,15 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source additions. The prefill kernel rescales its MFMA accumulators with
+# VALU multiplies on a rarely taken path; in the AGPR form the register
+# allocator copies all 128 accumulators between AGPRs and VGPRs on every tile
+# to serve that path, so its MFMAs are selected in the VGPR form.
+EXTRA_FLAGS = {
+    "prefill_attention": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+}
+
+
 def sources() -> list[Path]:
     return sorted(list(CSRC_DIR.glob("*.hip")) + list(CSRC_DIR.glob("*.cpp")))
 
@@ -54,7 +63,7 @@ def build(jobs: int = 8) -> Path:
     for src in sources():
         obj = OBJ_DIR / (src.stem + ".o")
         objs.append(obj)
-        cmd = [HIPCC, *HIP_FLAGS, "-c", str(src), "-o", str(obj)]
+        cmd = [HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src.stem, []), "-c", str(src), "-o", str(obj)]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE,
                                             stderr=subprocess.PIPE, text=True)))
         if len(procs) >= jobs:
