@@ -175,6 +175,20 @@ __device__ __forceinline__ void copy_row_pair(uint64_t src, uint32_t lds_addr) {
       : [lds] "s"(lds_addr), [src] "v"(src));
 }
 
+// One 4-byte-per-lane LDS copy: LDS bytes [lds_addr, +256) from the
+// per-lane addresses src (global_load_lds_dword); waited for like
+// copy_row_pair.
+__device__ __forceinline__ void copy_dwords(const void *src, uint32_t lds_addr) {
+  uint32_t m0_saved;
+  asm volatile(
+      "s_mov_b32 %[m0s], m0\n\t"
+      "s_mov_b32 m0, %[lds]\n\t"
+      "global_load_lds_dword %[src], off\n\t"
+      "s_mov_b32 m0, %[m0s]"
+      : [m0s] "=&s"(m0_saved)
+      : [lds] "s"(lds_addr), [src] "v"(src));
+}
+
 // Waits for every vector memory operation of this wave, the copies
 // included (s_waitcnt vmcnt(0); a builtin rather than inline asm so the
 // compiler's own counter bookkeeping sees it as well).
@@ -205,6 +219,7 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   __shared__ uint4 s_v1[kTileBytes / 16];
   __shared__ uint32_t s_valid[2][kPrefillWaves];      // bit j: key 16w + j of the stage is readable
   __shared__ uint4 s_rows[kPrefillWaves][kCopyKeys];  // {K address, V address} per copied key
+  __shared__ int32_t s_pages[2][kPrefillWaves][kWave];  // page-table entry per copied key (lane % 16)
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -262,44 +277,44 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int32_t *pt_row = paged ? p.page_table + (int64_t)b * c.max_pages_per_seq
                                 : reinterpret_cast<const int32_t *>(p.q);
   const int key_lane = lane & (kCopyKeys - 1);
-  auto lookup_page = [&](int kt) __attribute__((always_inline)) -> int32_t {
+  // Address of the page-table entry of key kt + 16w + lane % 16.
+  auto page_entry = [&](int kt) __attribute__((always_inline)) -> const int32_t * {
     int kp = kt + kCopyKeys * wave + key_lane;
     kp = kp < prior ? kp : prior - 1;  // chunk keys: any in-bounds slot
     kp = kp < 0 ? 0 : kp;
-    int slot = 0;
-    if (paged) {
-      const int lp = div_small(kp, c.page_size, inv_page);
-      slot = lp - div_small(lp, c.max_pages_per_seq, inv_pages) * c.max_pages_per_seq;
-    }
-    return pt_row[slot];
+    // Without a prior context page_size = max_pages = 1 and pt_row is any
+    // readable word, so the arithmetic needs no branch.
+    const int lp = div_small(kp, c.page_size, inv_page);
+    const int slot = lp - div_small(lp, c.max_pages_per_seq, inv_pages) * c.max_pages_per_seq;
+    return pt_row + (paged ? slot : 0);
   };
-  const uint16_t *chunk_k = p.k, *chunk_v = p.v;
-  const int64_t layer_rows = (int64_t)p.layer * c.num_pages;
+  // Row r of this head starts at base + (r << kRowShift) bytes in both the
+  // chunk tensor ([B][Lq][Hk][D], base = row 0 of sequence b) and the cache
+  // layer ([pages * page_size][Hk][D], base = row 0 of the layer).
+  constexpr int kRowShift = 12;  // log2(Hk * D * 2) for Hk = 8, D = 256
+  const uint64_t chunk_k = reinterpret_cast<uint64_t>(p.k + ((int64_t)b * Lq * Hk + head) * kDim);
+  const uint64_t chunk_v = reinterpret_cast<uint64_t>(p.v + ((int64_t)b * Lq * Hk + head) * kDim);
+  const int64_t layer_elems = (int64_t)p.layer * c.num_pages * c.page_size * Hk * kDim;
+  const uint64_t cache_k =
+      paged ? reinterpret_cast<uint64_t>(p.cache_k + layer_elems + head * kDim) : chunk_k;
+  const uint64_t cache_v =
+      paged ? reinterpret_cast<uint64_t>(p.cache_v + layer_elems + head * kDim) : chunk_v;
   // Byte addresses of one key's K and V rows for this head, and whether the
   // key can be read (in range, on a mapped page). Unreadable keys point at
-  // the first chunk row, which always exists, and are masked later.
+  // the first chunk row, which always exists, and are masked later. Written
+  // without branches so the compiler can interleave it with MFMAs.
   auto resolve = [&](int kt, int32_t phys, uint4 &rows_out) __attribute__((always_inline)) -> bool {
     const int kp = kt + kCopyKeys * wave + key_lane;
-    int64_t elem;
-    const uint16_t *kb;
-    const uint16_t *vb;
-    bool ok;
-    if (kp >= prior) {
-      ok = kp <= wg_last;
-      elem = (((int64_t)b * Lq + (ok ? kp - prior : 0)) * Hk + head) * kDim;
-      kb = chunk_k;
-      vb = chunk_v;
-    } else {
-      const int lp = div_small(kp, c.page_size, inv_page);
-      ok = paged && phys >= 0 && phys < c.num_pages;
-      const int64_t crow = (layer_rows + phys) * c.page_size + (kp - lp * c.page_size);
-      elem = (crow * Hk + head) * kDim;
-      kb = ok ? p.cache_k : chunk_k;
-      vb = ok ? p.cache_v : chunk_v;
-      if (!ok) elem = ((int64_t)b * Lq * Hk + head) * kDim;
-    }
-    const uint64_t ka = reinterpret_cast<uint64_t>(kb + elem);
-    const uint64_t va = reinterpret_cast<uint64_t>(vb + elem);
+    const bool is_chunk = kp >= prior;
+    const int lp = div_small(kp, c.page_size, inv_page);
+    const bool cache_ok = paged & (phys >= 0) & (phys < c.num_pages);
+    const bool ok = (is_chunk & (kp <= wg_last)) | (!is_chunk & cache_ok);
+    const uint32_t crow = (uint32_t)(phys * c.page_size + (kp - lp * c.page_size));
+    const uint32_t row = ok ? (is_chunk ? (uint32_t)(kp - prior) : crow) : 0u;
+    const bool use_cache = ok & !is_chunk;
+    const uint64_t off = (uint64_t)row << kRowShift;
+    const uint64_t ka = (use_cache ? cache_k : chunk_k) + off;
+    const uint64_t va = (use_cache ? cache_v : chunk_v) + off;
     rows_out = make_uint4((uint32_t)ka, (uint32_t)(ka >> 32), (uint32_t)va, (uint32_t)(va >> 32));
     return ok;
   };
@@ -324,8 +339,10 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     uint4 rows;
     const bool ok = resolve(kt, phys, rows);
     const uint32_t ok_bits = (uint32_t)__builtin_amdgcn_ballot_w64(ok) & 0xFFFFu;
-    if (lane < kCopyKeys) s_rows[wave][lane] = rows;
-    if (lane == 0) s_valid[S][wave] = ok_bits;
+    // Lanes with equal lane % 16 hold equal rows, so every lane stores
+    // (no divergent branch in the way of instruction scheduling).
+    s_rows[wave][key_lane] = rows;
+    s_valid[S][wave] = ok_bits;
     uint4 rr[kCopyKeys / 2];
 #pragma unroll
     for (int a = 0; a < kCopyKeys / 2; ++a) rr[a] = s_rows[wave][2 * a + half];
@@ -370,15 +387,32 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   for (int d = 0; d < DB; ++d) acc[d] = f32x16_t{};
 
   // One block of 32 keys: S^T, masked softmax, O^T += V^T P^T.
-  // The copy of the next tile rides on the block's score MFMAs (issued
-  // even when the block itself is skipped).
-  auto attend_block = [&](auto kimm, const char *vbase, int kb_lo, uint32_t valid32, bool copy,
-                          const uint64_t (&src)[kCopyKeys / 2], uint32_t dst) __attribute__((always_inline)) {
+  // Next-tile work rides on the two blocks of a tile: the row addresses
+  // are resolved (next_rows) while block 0's score MFMAs run, and the 16
+  // copies are issued between block 1's score MFMAs. Both happen even when
+  // a block itself is skipped.
+  uint64_t ksrc[kCopyKeys / 2], vsrc[kCopyKeys / 2];
+  auto issue_copies = [&](auto st) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+#pragma unroll
+    for (int c = 0; c < kCopyKeys / 2; ++c) {
+      copy_row_pair(ksrc[c], k_dst[S ^ 1] + c * 2 * kRowBytes);
+      copy_row_pair(vsrc[c], v_dst[S ^ 1] + c * 2 * kRowBytes);
+    }
+  };
+  auto attend_block = [&](auto st, auto blk, const char *vbase, int kb_lo, uint32_t valid32,
+                          bool copy, auto &&next_rows) __attribute__((always_inline)) {
+    constexpr int S = decltype(st)::value;
+    constexpr int kBlk = decltype(blk)::value;
+    constexpr int kImm = S * kTileBytes + kBlk * 32 * kRowBytes;
     const int kb_hi = kb_lo + 31;
     if (!wave_has_rows || kb_lo > wave_qmax || (p.window > 0 && kb_hi <= wave_qmin - p.window)) {
       if (copy) {
-#pragma unroll
-        for (int c = 0; c < kCopyKeys / 2; ++c) copy_row_pair(src[c], dst + c * 2 * kRowBytes);
+        if constexpr (kBlk == 0) {
+          next_rows();
+        } else {
+          issue_copies(st);
+        }
       }
       return;
     }
@@ -386,18 +420,33 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
                       (p.window == 0 || kb_lo > wave_qmax - p.window);
     // S^T[key m][row n] = sum_d K[m][d] Q[n][d].
     u32x4v_t kf[KS];
-    read_kfrags<decltype(kimm)::value>(k_addr, kf);
+    read_kfrags<kImm>(k_addr, kf);
     f32x16_t s_acc = f32x16_t{};
-    // The next tile's copies ride between the first eight MFMAs.
     auto step_s = [&](auto sc) __attribute__((always_inline)) {
       constexpr int s = decltype(sc)::value;
       kfrag_ready<s>(kf[s]);
       s_acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s]),
                                                       __builtin_bit_cast(bf16x8_t, qreg[s]), s_acc,
                                                       0, 0, 0);
-      if (s < kCopyKeys / 2 && copy) copy_row_pair(src[s % 8], dst + (s % 8) * 2 * kRowBytes);
+      if constexpr (kBlk == 1) {
+        if (copy) {
+          if constexpr (s % 2 == 0) {
+            copy_row_pair(ksrc[s / 2], k_dst[S ^ 1] + (s / 2) * 2 * kRowBytes);
+          } else {
+            copy_row_pair(vsrc[s / 2], v_dst[S ^ 1] + (s / 2) * 2 * kRowBytes);
+          }
+        }
+      }
     };
     static_for<0, KS>(step_s);
+    if constexpr (kBlk == 0) {
+      if (copy) next_rows();
+      // Interleave the address work with the score MFMAs.
+      static_for<0, KS>([](auto) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
+      });
+    }
     // Lane holds keys m = (i/4)*8 + 4*half + i%4, i = 0..15, of row n.
     float sc[16];
     float tmax = -INFINITY;
@@ -461,27 +510,14 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     }
   };
 
-  auto compute_tile = [&](auto st, int kt, bool copy, const uint64_t (&ksrc)[kCopyKeys / 2],
-                          const uint64_t (&vsrc)[kCopyKeys / 2]) __attribute__((always_inline)) {
-    constexpr int S = decltype(st)::value;
-    const char *vbase = reinterpret_cast<const char *>(S == 0 ? s_v0 : s_v1);
-    const uint4 vw = *reinterpret_cast<const uint4 *>(&s_valid[S][0]);
-    attend_block(std::integral_constant<int, S * kTileBytes>{}, vbase, kt, vw.x | (vw.y << 16),
-                 copy, ksrc, k_dst[S ^ 1]);
-    attend_block(std::integral_constant<int, S * kTileBytes + 32 * kRowBytes>{},
-                 vbase + 32 * kRowBytes, kt + 32, vw.z | (vw.w << 16), copy, vsrc, v_dst[S ^ 1]);
-  };
-
   // ---- pipeline: copy tile i+1 and look up tile i+2 while computing i -----
-  uint64_t ksrc[kCopyKeys / 2], vsrc[kCopyKeys / 2];
-  int32_t phys = lookup_page(tile0);
-  prepare_copy(Stage<0>{}, tile0, phys, ksrc, vsrc);
-#pragma unroll
-  for (int c = 0; c < kCopyKeys / 2; ++c) {
-    copy_row_pair(ksrc[c], k_dst[0] + c * 2 * kRowBytes);
-    copy_row_pair(vsrc[c], v_dst[0] + c * 2 * kRowBytes);
-  }
-  if (n_tiles > 1) phys = lookup_page(tile0 + kTileKeys);
+  // The page-table entries of tile t land in s_pages[t & 1] by LDS copy,
+  // issued two tiles ahead, so no vector register waits on them.
+  const uint32_t page_dst[2] = {(uint32_t)wave_uniform(lds_addr(&s_pages[0][wave][0])),
+                                (uint32_t)wave_uniform(lds_addr(&s_pages[1][wave][0]))};
+  prepare_copy(Stage<0>{}, tile0, *page_entry(tile0), ksrc, vsrc);
+  issue_copies(Stage<1>{});  // into stage 0
+  copy_dwords(page_entry(tile0 + kTileKeys), page_dst[1]);
   auto step = [&](auto st, int it) __attribute__((always_inline)) {
     constexpr int S = decltype(st)::value;
     const int kt = tile0 + it * kTileKeys;
@@ -489,17 +525,27 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     // Every wave has also finished tile it-1, so stage S^1 is free.
     wait_copies();
     __syncthreads();
-    const bool copy = it + 1 < n_tiles;
-    if (copy) {
-      prepare_copy(Stage<S ^ 1>{}, kt + kTileKeys, phys, ksrc, vsrc);
-      if (it + 2 < n_tiles) phys = lookup_page(kt + 2 * kTileKeys);
-    }
-    compute_tile(st, kt, copy, ksrc, vsrc);
+    // The copy after the last tile reads keys past the workgroup's range,
+    // which resolve to the (always readable) first chunk row: the loop has
+    // no branches around its copies.
+    constexpr bool copy = true;
+    const int32_t next_phys = s_pages[S ^ 1][wave][lane];
+    auto next_rows = [&]() __attribute__((always_inline)) {
+      prepare_copy(Stage<S ^ 1>{}, kt + kTileKeys, next_phys, ksrc, vsrc);
+      copy_dwords(page_entry(kt + 2 * kTileKeys), page_dst[S]);
+    };
+    const char *vbase = reinterpret_cast<const char *>(S == 0 ? s_v0 : s_v1);
+    const uint4 vw = *reinterpret_cast<const uint4 *>(&s_valid[S][0]);
+    attend_block(st, std::integral_constant<int, 0>{}, vbase, kt, vw.x | (vw.y << 16), copy,
+                 next_rows);
+    attend_block(st, std::integral_constant<int, 1>{}, vbase + 32 * kRowBytes, kt + 32,
+                 vw.z | (vw.w << 16), copy, next_rows);
   };
   for (int it = 0; it < n_tiles; it += 2) {
     step(Stage<0>{}, it);
     if (it + 1 < n_tiles) step(Stage<1>{}, it + 1);
   }
+  wait_copies();  // no copy may still be writing LDS when the workgroup exits
 
   // Normalise and store: lane holds dims 32d + (i/4)*8 + 4*half + i%4 of row n.
   l_run += lane_xor<32>(l_run);
