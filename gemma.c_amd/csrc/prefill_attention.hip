@@ -29,14 +29,24 @@
 //     hands lane i of a 16-lane group V[k0 + e][n0 + i] (e = 0..3) from four
 //     rows x 32 bytes, which this layout spreads over all banks. The
 //     transposing read turns row-major V into the V^T operand directly.
-// Tile t+1 is copied while tile t is computed; one barrier per tile.
+// Tile t+1 is copied while tile t is computed; one barrier per tile. The
+// copies are issued between block 1's score MFMAs (inline asm, so the
+// compiler neither serialises them nor waits on them; each wave waits for
+// its own copies right before the barrier), the next tile's row addresses
+// are resolved between block 0's score MFMAs, and the page-table entries
+// those need arrive in LDS by a 4-byte copy issued two tiles ahead.
+// Each score block first issues all 16 of its K-fragment reads (into AGPRs),
+// then its MFMA chain, so LDS latency is paid once per block. The MFMAs use
+// the VGPR accumulator form (a build flag for this file): with AGPR
+// accumulators the rarely taken rescale path made the compiler copy all 128
+// accumulators between register files on every tile.
 // Softmax maxima are updated lazily: the running max moves (and the
 // accumulators are rescaled) only when a row's new maximum exceeds it by
 // more than 8 in log2 units, so exp2 arguments stay <= 8 and the result is
-// unchanged up to rounding. Blocks of 32 keys that no row of a wave sees are
-// skipped, and blocks every row sees skip the mask. Blocks are ordered
-// head-fastest so the workgroups of one kv head land on one XCD and share its
-// L2 as they stream the same keys.
+// unchanged up to rounding. Blocks of 32 keys that no row of a wave sees
+// skip their MFMAs (not their share of the copies), and blocks every row
+// sees skip the mask. Blocks are ordered head-fastest so the workgroups of
+// one kv head land on one XCD and share its L2 as they stream the same keys.
 #include "gemma4_device.hpp"
 
 #include "gemma4_flash_attention.h"
