@@ -222,14 +222,26 @@ using Stage = std::integral_constant<int, kSt>;
 __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(PrefillParams p) {
   constexpr int KS = kDim / 16;        // k-steps of S^T (dims)
   constexpr int DB = kDim / 32;        // 32-dim blocks of O^T
-  // K stages are read only by score_block (inline asm), so one array holds
-  // both; 512-byte alignment keeps the XOR swizzle out of the base address.
-  __shared__ __attribute__((aligned(1024))) uint4 s_k[2][kTileBytes / 16];
-  __shared__ uint4 s_v0[kTileBytes / 16];
-  __shared__ uint4 s_v1[kTileBytes / 16];
-  __shared__ uint32_t s_valid[2][kPrefillWaves];      // bit j: key 16w + j of the stage is readable
-  __shared__ uint4 s_rows[kPrefillWaves][kCopyKeys];  // {K address, V address} per copied key
-  __shared__ int32_t s_pages[2][kPrefillWaves][kWave];  // page-table entry per copied key (lane % 16)
+  // One LDS object with a fixed layout. V stages come first: the
+  // transposing reads address them with a 16-bit immediate offset, which
+  // reaches only the first 64 KiB. K stages are read by read_kfrags (inline
+  // asm, base in a register); their 512-byte alignment keeps the XOR
+  // swizzle out of the base address. All LDS copies are inline asm, so the
+  // compiler needs no per-object aliasing to keep them apart from its reads.
+  struct Lds {
+    uint4 v[2][kTileBytes / 16];
+    uint4 k[2][kTileBytes / 16];
+    uint32_t valid[2][kPrefillWaves];      // bit j: key 16w + j of the stage is readable
+    uint4 rows[kPrefillWaves][kCopyKeys];  // {K address, V address} per copied key
+    int32_t pages[2][kPrefillWaves][kWave];  // page-table entry per copied key (lane % 16)
+  };
+  __shared__ __attribute__((aligned(1024))) Lds lds;
+  uint4 *const s_v0 = lds.v[0];
+  uint4 *const s_v1 = lds.v[1];
+  auto &s_k = lds.k;
+  auto &s_valid = lds.valid;
+  auto &s_rows = lds.rows;
+  auto &s_pages = lds.pages;
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -457,26 +469,32 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
       });
     }
-    // Lane holds keys m = (i/4)*8 + 4*half + i%4, i = 0..15, of row n.
+    // Lane holds keys m = (i/4)*8 + 4*half + i%4, i = 0..15, of row n. The
+    // maximum is taken over the raw scores (q_scale > 0) and the scale is
+    // folded into the exp2 argument.
     float sc[16];
-    float tmax = -INFINITY;
     if (full) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        sc[i] = s_acc[i] * p.q_scale;
-        tmax = fmaxf(tmax, sc[i]);
-      }
+      for (int i = 0; i < 16; ++i) sc[i] = s_acc[i];
     } else {
+      // Visible keys of this row as a 32-bit mask over the block: readable,
+      // at or before the row, and inside its window.
+      const int hi = qpos - kb_lo;        // last visible key index
+      const int lo = win_lo + 1 - kb_lo;  // first visible key index
+      const uint32_t below = hi < 0 ? 0u : (hi >= 31 ? 0xFFFFFFFFu : (2u << hi) - 1u);
+      const uint32_t above = lo <= 0 ? 0xFFFFFFFFu : (lo > 31 ? 0u : 0xFFFFFFFFu << lo);
+      const uint32_t vis = (row_ok ? valid32 & below & above : 0u) >> (4 * half);
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int m = (i / 4) * 8 + 4 * half + (i % 4);
-        const int kp = kb_lo + m;
-        const bool vis = row_ok & (((valid32 >> m) & 1u) != 0) & (kp <= qpos) & (kp > win_lo);
-        sc[i] = vis ? s_acc[i] * p.q_scale : -INFINITY;
-        tmax = fmaxf(tmax, sc[i]);
+        const int m = (i / 4) * 8 + (i % 4);
+        sc[i] = (vis >> m) & 1u ? s_acc[i] : -INFINITY;
       }
     }
-    tmax = fmaxf(tmax, lane_xor<32>(tmax));
+    float tmax = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+#pragma unroll
+    for (int i = 3; i < 15; i += 2) tmax = fmaxf(fmaxf(tmax, sc[i]), sc[i + 1]);
+    tmax = fmaxf(tmax, sc[15]);
+    tmax = fmaxf(tmax, lane_xor<32>(tmax)) * p.q_scale;
     // Lazy maximum: move it (and rescale) only when a row outgrew it by more
     // than the slack; otherwise exp2 arguments stay below the slack.
     if (__builtin_amdgcn_ballot_w64(tmax > m_run + kRescaleSlack) != 0) {
@@ -491,8 +509,8 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     uint32_t pw[8];
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const float p0 = __builtin_amdgcn_exp2f(sc[i] - m_use);
-      const float p1 = __builtin_amdgcn_exp2f(sc[i + 1] - m_use);
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[i], p.q_scale, -m_use));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[i + 1], p.q_scale, -m_use));
       l_run += p0 + p1;
       pw[i / 2] = cvt_pk_bf16(p0, p1);
     }
