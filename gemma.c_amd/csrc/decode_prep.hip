@@ -15,6 +15,7 @@
 // prepared q rows and cache rows.
 #include "gemma4_device.hpp"
 #include "decode_common.hpp"
+#include "prep_common.hpp"
 
 #include "gemma4_flash_attention.h"
 
@@ -22,8 +23,6 @@
 
 namespace gemma4 {
 namespace {
-
-constexpr float kRmsEps = 1.0e-6f;  // GEMMA4_RMS_NORM_EPS (src/gemma4.h:29)
 
 struct PrepParams {
   uint16_t *q_prepared;
@@ -42,76 +41,6 @@ struct PrepParams {
   int32_t layer;
 };
 
-__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
-
-__device__ __forceinline__ float wave_sum(float v) {
-  v += lane_xor<1>(v);
-  v += lane_xor<2>(v);
-  v += lane_xor<4>(v);
-  v += lane_xor<8>(v);
-  v += lane_xor<16>(v);
-  v += lane_xor<32>(v);
-  return v;
-}
-
-// rsqrt(mean(x^2) + eps) of one head (src/gemma4_rmsnorm.cu:90-101).
-template <int kDim>
-__device__ __forceinline__ float head_rms_scale(const float (&x)[kDim / kWave]) {
-  float sum_sq = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kDim / kWave; ++i) sum_sq = fmaf(x[i], x[i], sum_sq);
-  sum_sq = wave_sum(sum_sq);
-  return 1.0f / sqrtf(sum_sq / (float)kDim + kRmsEps);
-}
-
-// Learned RMSNorm, then RoPE over the first kRotary dims (pairs d and
-// d + kRotary/2), plain normalised tail (src/gemma4_flash_attention_decode.cu:233-269).
-template <int kDim, int kRotary>
-__device__ __forceinline__ void store_weighted_rope(uint16_t *out, const float (&x)[kDim / kWave],
-                                                    const uint16_t *weight, const float *cos_row,
-                                                    const float *sin_row, int lane) {
-  constexpr int kPer = kDim / kWave;
-  constexpr int kHalf = kRotary / 2;
-  constexpr int kPairSteps = kHalf / kWave;  // lane-strided steps inside the first half
-  const float scale = head_rms_scale<kDim>(x);
-  float y[kPer];
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) y[i] = x[i] * scale * bf16_to_f32(weight[lane + i * kWave]);
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int d = lane + i * kWave;
-    float r;
-    if (i < kPairSteps) {  // d in the first rotary half
-      const float c = cos_row[d], s = sin_row[d];
-      r = fmaf(-y[i + kPairSteps], s, y[i] * c);
-    } else if (i < 2 * kPairSteps) {  // d in the second rotary half
-      const float c = cos_row[d - kHalf], s = sin_row[d - kHalf];
-      r = fmaf(y[i - kPairSteps], s, y[i] * c);
-    } else {
-      r = y[i];
-    }
-    out[d] = (uint16_t)f32_to_bf16_bits(r);
-  }
-}
-
-// Scale-free RMSNorm (src/gemma4_flash_attention_decode.cu:271-283).
-template <int kDim>
-__device__ __forceinline__ void store_scale_free(uint16_t *out, const float (&x)[kDim / kWave],
-                                                 int lane) {
-  const float scale = head_rms_scale<kDim>(x);
-#pragma unroll
-  for (int i = 0; i < kDim / kWave; ++i)
-    out[lane + i * kWave] = (uint16_t)f32_to_bf16_bits(x[i] * scale);
-}
-
-// Waves per workgroup: the query heads, then K and V for the sliding
-// geometry; for the global geometry (16 query heads) wave 0 also does K and
-// the K-derived V, keeping the workgroup at 16 waves.
-template <int kHeads, bool kHasV>
-constexpr int prep_waves() {
-  return kHasV ? kQueryHeads / kHeads + 2 : kQueryHeads / kHeads;
-}
-
 template <int kHeads, int kDim, int kRotary, bool kHasV>
 __global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void decode_prep_append_kernel(
     PrepParams p) {
@@ -128,14 +57,10 @@ __global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void decode_
   const float *sin_row = p.sin + (int64_t)position * (kRotary / 2);
 
   float x[kPer];
-  auto load_head = [&](const uint16_t *src) {
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) x[i] = bf16_to_f32(src[lane + i * kWave]);
-  };
 
   if (wave < kGroup) {
     const int64_t off = ((int64_t)b * kQueryHeads + head * kGroup + wave) * kDim;
-    load_head(p.q + off);
+    load_head<kDim>(p.q + off, x, lane);
     store_weighted_rope<kDim, kRotary>(p.q_prepared + off, x, p.q_norm_weight, cos_row, sin_row,
                                        lane);
     if (kHasV || wave != 0) return;
@@ -153,12 +78,12 @@ __global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void decode_
   const int64_t dst = (row * kHeads + head) * kDim;
   const int64_t src = ((int64_t)b * kHeads + head) * kDim;
   if (k_wave) {
-    load_head(p.k + src);
+    load_head<kDim>(p.k + src, x, lane);
     store_weighted_rope<kDim, kRotary>(p.cache_k + dst, x, p.k_norm_weight, cos_row, sin_row,
                                        lane);
     if constexpr (!kHasV) store_scale_free<kDim>(p.cache_v + dst, x, lane);
   } else {
-    load_head(p.v + src);
+    load_head<kDim>(p.v + src, x, lane);
     store_scale_free<kDim>(p.cache_v + dst, x, lane);
   }
 }

@@ -1,0 +1,348 @@
+// Prefill self-attention launchers with Q/K/V preparation, gfx950: the drop-in
+// for gemma4_flash_attention_{sliding,global}_fwd_bf16_norm_rope
+// (src/gemma4_flash_attention.cuh:9-45, src/gemma4_flash_attention_prefill.cu:1110-1257).
+// Each launcher runs two kernels on the caller's stream:
+//   1. prefill_prep_kernel: per (token row, kv head) Q and K get learned
+//      RMSNorm + split-half RoPE at the row's absolute position, V gets
+//      scale-free RMSNorm (the 1x512 geometry derives V from the raw K), into
+//      the caller's q/k/v_prepared buffers
+//      (src/gemma4_flash_attention_prefill.cu:1023-1101);
+//   2. causal attention over the prepared rows (seqlen_q == seqlen_k):
+//      the 8x256 geometry reuses the chunk kernel (no prior context), the
+//      1x512 geometry runs prefill_d512_kernel below.
+//
+// prefill_d512_kernel: 16 query heads share one 512-dim KV head. A wave owns
+// one query row and all 16 heads (16 MFMA columns) on
+// v_mfma_f32_16x16x32_bf16, computing S^T = K Q^T (16 keys x 16 heads per
+// block, 16 k-steps of 32 dims) and O^T = V^T P^T (32 dim blocks of 16). In
+// the 16x16 accumulator lane l holds head l % 16 and four keys (or dims)
+// 4 (l/16) + i, so P^T feeds the second MFMA from registers when its 32-key
+// contraction order is permuted to {4g..4g+3, 16+4g..16+4g+3} for lane
+// group g, and V^T is read in that order by two ds_read_b64_tr_b16 per
+// operand. O^T is 128 fp32 per lane, Q^T 64 registers. A workgroup is four
+// consecutive rows that share 32-key K/V tiles staged in LDS (K chunk c of
+// key k at c ^ (k & 15), V chunk c at c ^ ((k & 7) << 1), 16-byte chunks,
+// so the operand reads are bank-conflict free). The lazy online softmax of
+// the chunk kernel (maximum moved only when it grows by more than 8 in
+// log2 units). This geometry is outside the BASELINE configs; the kernel is
+// written for parity, not tuned.
+#include "gemma4_device.hpp"
+#include "prep_common.hpp"
+
+#include "gemma4_flash_attention.h"
+
+#include <math.h>
+
+namespace gemma4 {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+struct PrefillPrepParams {
+  uint16_t *q_prepared;  // [rows][16][D]
+  uint16_t *k_prepared;  // [rows][Hk][D]
+  uint16_t *v_prepared;
+  const uint16_t *q;
+  const uint16_t *k;
+  const uint16_t *v;     // null for the 1x512 geometry (V from K)
+  const uint16_t *q_norm_weight;
+  const uint16_t *k_norm_weight;
+  const float *cos;
+  const float *sin;
+  const int32_t *token_position;  // [rows]
+};
+
+// Workgroup (token row, kv head), one wave per prepared head; a negative
+// position skips the row (src/gemma4_flash_attention_prefill.cu:1049-1051).
+template <int kHeads, int kDim, int kRotary, bool kHasV>
+__global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void prefill_prep_kernel(
+    PrefillPrepParams p) {
+  constexpr int kGroup = kQueryHeads / kHeads;
+  constexpr int kPer = kDim / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = wave_uniform(threadIdx.x / kWave);
+  const int64_t row = blockIdx.x;
+  const int head = blockIdx.y;
+  const int32_t position = wave_uniform(p.token_position[row]);
+  if (position < 0) return;
+  const float *cos_row = p.cos + (int64_t)position * (kRotary / 2);
+  const float *sin_row = p.sin + (int64_t)position * (kRotary / 2);
+  float x[kPer];
+  if (wave < kGroup) {
+    const int64_t off = (row * kQueryHeads + head * kGroup + wave) * kDim;
+    load_head<kDim>(p.q + off, x, lane);
+    store_weighted_rope<kDim, kRotary>(p.q_prepared + off, x, p.q_norm_weight, cos_row, sin_row,
+                                       lane);
+    if (kHasV || wave != 0) return;
+  }
+  const int64_t off = (row * kHeads + head) * kDim;
+  const bool k_wave = kHasV ? wave == kGroup : wave == 0;
+  if (k_wave) {
+    load_head<kDim>(p.k + off, x, lane);
+    store_weighted_rope<kDim, kRotary>(p.k_prepared + off, x, p.k_norm_weight, cos_row, sin_row,
+                                       lane);
+    if constexpr (!kHasV) store_scale_free<kDim>(p.v_prepared + off, x, lane);
+  } else {
+    load_head<kDim>(p.v + off, x, lane);
+    store_scale_free<kDim>(p.v_prepared + off, x, lane);
+  }
+}
+
+// ---- 1x512 causal self-attention ---------------------------------------
+constexpr int kD512 = 512;
+constexpr int kD512Rows = 4;          // query rows (one per wave) per workgroup
+constexpr int kD512Threads = kD512Rows * kWave;
+constexpr int kD512Tile = 32;         // keys per LDS tile
+constexpr int kD512RowBytes = kD512 * 2;
+constexpr int kD512Chunks = kD512RowBytes / 16;  // 16-byte chunks per row
+constexpr float kD512Slack = 8.0f;
+
+struct D512Params {
+  uint16_t *out;        // [B][L][16][512]
+  const uint16_t *q;    // [B][L][16][512]
+  const uint16_t *k;    // [B][L][1][512]
+  const uint16_t *v;
+  int32_t seq_len;
+  float q_scale;        // softmax_scale * log2(e)
+};
+
+__device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Params p) {
+  constexpr int KS = kD512 / 32;  // 32-dim k-steps of S^T
+  constexpr int DB = kD512 / 16;  // 16-dim blocks of O^T
+  __shared__ uint4 s_k[kD512Tile * kD512Chunks];
+  __shared__ uint4 s_v[kD512Tile * kD512Chunks];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = wave_uniform(t >> 6);
+  const int head = lane & 15;   // MFMA column
+  const int g = lane >> 4;      // lane group: keys / dims 4g..4g+3 of the accumulator
+  const int b = blockIdx.y;
+  const int L = p.seq_len;
+  const int r0 = blockIdx.x * kD512Rows;
+  const int row = r0 + wave;
+  const bool row_ok = row < L;
+  const int last_key = min(r0 + kD512Rows, L) - 1;  // last key any row of the workgroup sees
+
+  // Q^T operand: lane holds Q[row][head][32 s + 8 g .. +8] for k-step s.
+  uint4 qreg[KS];
+  {
+    const uint16_t *qrow = p.q + (((int64_t)b * L + (row_ok ? row : 0)) * kQueryHeads + head) * kD512;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      qreg[s] = row_ok ? load128(qrow + 32 * s + 8 * g) : make_uint4(0, 0, 0, 0);
+  }
+
+  float m_run = -INFINITY, l_run = 0.0f;
+  f32x4_t acc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) acc[d] = f32x4_t{};
+
+  const uint16_t *kseq = p.k + (int64_t)b * L * kD512;
+  const uint16_t *vseq = p.v + (int64_t)b * L * kD512;
+  const int n_tiles = last_key / kD512Tile + 1;
+  for (int tile = 0; tile < n_tiles; ++tile) {
+    const int kt = tile * kD512Tile;
+    // Stage the tile: thread t copies chunk t % 64 of keys t/64 + 4i.
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kD512Tile * kD512Chunks / kD512Threads; ++i) {
+      const int key = t / kD512Chunks + (kD512Threads / kD512Chunks) * i;
+      const int c = t % kD512Chunks;
+      const int src_key = min(kt + key, L - 1);  // past the end: any row, masked below
+      const uint4 kv = load128(kseq + (int64_t)src_key * kD512 + c * 8);
+      const uint4 vv = load128(vseq + (int64_t)src_key * kD512 + c * 8);
+      s_k[key * kD512Chunks + (c ^ (key & 15))] = kv;
+      s_v[key * kD512Chunks + (c ^ ((key & 7) << 1))] = vv;
+    }
+    __syncthreads();
+    if (!row_ok || kt > row) continue;  // uniform per wave; the barriers are at the loop top
+
+    // Scores of the two 16-key blocks: lane holds head `head`, keys
+    // 16 blk + 4 g + i.
+    f32x4_t sblk[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const int key = 16 * blk + (lane & 15);
+      f32x4_t s_acc = f32x4_t{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int c = 4 * s + g;
+        const uint4 kf = s_k[key * kD512Chunks + (c ^ (key & 15))];
+        s_acc = mfma16(kf, qreg[s], s_acc);
+      }
+      sblk[blk] = s_acc;
+    }
+    float sc[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int kp = kt + 16 * (j / 4) + 4 * g + (j % 4);
+      const float x = sblk[j / 4][j % 4];
+      sc[j] = kp <= row ? x : -INFINITY;
+      tmax = fmaxf(tmax, sc[j]);
+    }
+    tmax = fmaxf(tmax, lane_xor<16>(tmax));
+    tmax = fmaxf(tmax, lane_xor<32>(tmax)) * p.q_scale;
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + kD512Slack) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) acc[d] *= alpha;
+      m_run = m_new;
+    }
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    uint32_t pw[4];
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[j], p.q_scale, -m_use));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[j + 1], p.q_scale, -m_use));
+      l_run += p0 + p1;
+      pw[j / 2] = pack_bf16x2(p0, p1);
+    }
+    const uint4 pb = make_uint4(pw[0], pw[1], pw[2], pw[3]);
+    // V^T operand of dim block d: lane i of group g reads rows k0 + j,
+    // dims 16 d + 4 q (j = (lane % 16) / 4, q = lane % 4) with k0 = 4 g
+    // and 16 + 4 g.
+    const int vj = (lane & 15) >> 2;
+    const int vq = lane & 3;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      uint2 half_op[2];
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int vrow = 16 * r + 4 * g + vj;
+        const int c = 2 * d + (vq >> 1);
+        const char *addr = reinterpret_cast<const char *>(s_v) + vrow * kD512RowBytes +
+                           ((c ^ ((vrow & 7) << 1)) << 4) + ((vq & 1) << 3);
+        typedef __attribute__((address_space(3))) i16x4_t lds_i16x4;
+        const i16x4_t tr = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4 *)(__attribute__((address_space(3))) const char *)(addr));
+        half_op[r] = __builtin_bit_cast(uint2, tr);
+      }
+      acc[d] = mfma16(make_uint4(half_op[0].x, half_op[0].y, half_op[1].x, half_op[1].y), pb,
+                      acc[d]);
+    }
+  }
+
+  // Normalise and store: lane holds head `head`, dims 16 d + 4 g + i.
+  l_run += lane_xor<16>(l_run);
+  l_run += lane_xor<32>(l_run);
+  if (!row_ok) return;
+  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+  uint16_t *orow = p.out + (((int64_t)b * L + row) * kQueryHeads + head) * kD512;
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+    uint2 o;
+    o.x = pack_bf16x2(acc[d][0] * inv, acc[d][1] * inv);
+    o.y = pack_bf16x2(acc[d][2] * inv, acc[d][3] * inv);
+    *reinterpret_cast<uint2 *>(orow + 16 * d + 4 * g) = o;
+  }
+}
+
+bool prefill_args_ok(const void *out, const void *qp, const void *kp, const void *vp,
+                     const void *q, const void *k, const void *position, int batch_size,
+                     int seqlen_q, int seqlen_k) {
+  // src/gemma4_flash_attention_prefill.cu:1131-1138, 1199-1205
+  return batch_size > 0 && seqlen_q > 0 && seqlen_q == seqlen_k && out != nullptr &&
+         qp != nullptr && kp != nullptr && vp != nullptr && q != nullptr && k != nullptr &&
+         position != nullptr && (int64_t)batch_size * seqlen_q <= 0x7fffffff;
+}
+
+}  // namespace
+}  // namespace gemma4
+
+using namespace gemma4;
+
+extern "C" hipError_t gemma4_flash_attention_sliding_fwd_bf16_norm_rope(
+    gemma4_bf16 *d_out, gemma4_bf16 *d_q_prepared, gemma4_bf16 *d_k_prepared,
+    gemma4_bf16 *d_v_prepared, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_v, const gemma4_bf16 *d_q_norm_weight,
+    const gemma4_bf16 *d_k_norm_weight, const float *d_cos, const float *d_sin,
+    const int32_t *d_token_position, int batch_size, int seqlen_q, int seqlen_k, int window_size,
+    float softmax_scale, hipStream_t stream) {
+  if (!prefill_args_ok(d_out, d_q_prepared, d_k_prepared, d_v_prepared, d_q, d_k,
+                       d_token_position, batch_size, seqlen_q, seqlen_k) ||
+      window_size <= 0 || d_v == nullptr || d_q_norm_weight == nullptr ||
+      d_k_norm_weight == nullptr || d_cos == nullptr || d_sin == nullptr) {
+    return hipErrorInvalidValue;
+  }
+  PrefillPrepParams pp{};
+  pp.q_prepared = reinterpret_cast<uint16_t *>(d_q_prepared);
+  pp.k_prepared = reinterpret_cast<uint16_t *>(d_k_prepared);
+  pp.v_prepared = reinterpret_cast<uint16_t *>(d_v_prepared);
+  pp.q = reinterpret_cast<const uint16_t *>(d_q);
+  pp.k = reinterpret_cast<const uint16_t *>(d_k);
+  pp.v = reinterpret_cast<const uint16_t *>(d_v);
+  pp.q_norm_weight = reinterpret_cast<const uint16_t *>(d_q_norm_weight);
+  pp.k_norm_weight = reinterpret_cast<const uint16_t *>(d_k_norm_weight);
+  pp.cos = d_cos;
+  pp.sin = d_sin;
+  pp.token_position = d_token_position;
+  // 8x256 geometry: RoPE over the whole head, V projection present.
+  hipLaunchKernelGGL((prefill_prep_kernel<8, 256, 256, true>),
+                     dim3(batch_size * seqlen_q, 8), dim3(prep_waves<8, true>() * kWave), 0,
+                     stream, pp);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  // Attention over the prepared rows: the chunk kernel without a prior
+  // context (only num_heads, head_dim and window_size of the config are read).
+  Gemma4KvCacheConfig c{};
+  c.num_layers = 1;
+  c.num_heads = 8;
+  c.head_dim = 256;
+  c.window_size = window_size;
+  return gemma4_flash_attention_prefill_chunk_paged_bf16(
+      d_out, d_q_prepared, d_k_prepared, d_v_prepared, nullptr, nullptr, nullptr, nullptr, c, 0,
+      batch_size, seqlen_q, softmax_scale, stream);
+}
+
+extern "C" hipError_t gemma4_flash_attention_global_fwd_bf16_norm_rope(
+    gemma4_bf16 *d_out, gemma4_bf16 *d_q_prepared, gemma4_bf16 *d_k_prepared,
+    gemma4_bf16 *d_v_prepared, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_q_norm_weight, const gemma4_bf16 *d_k_norm_weight, const float *d_cos,
+    const float *d_sin, const int32_t *d_token_position, int batch_size, int seqlen_q,
+    int seqlen_k, float softmax_scale, hipStream_t stream) {
+  if (!prefill_args_ok(d_out, d_q_prepared, d_k_prepared, d_v_prepared, d_q, d_k,
+                       d_token_position, batch_size, seqlen_q, seqlen_k) ||
+      d_q_norm_weight == nullptr || d_k_norm_weight == nullptr || d_cos == nullptr ||
+      d_sin == nullptr || batch_size > 65535 || !(softmax_scale > 0.0f)) {
+    return hipErrorInvalidValue;
+  }
+  PrefillPrepParams pp{};
+  pp.q_prepared = reinterpret_cast<uint16_t *>(d_q_prepared);
+  pp.k_prepared = reinterpret_cast<uint16_t *>(d_k_prepared);
+  pp.v_prepared = reinterpret_cast<uint16_t *>(d_v_prepared);
+  pp.q = reinterpret_cast<const uint16_t *>(d_q);
+  pp.k = reinterpret_cast<const uint16_t *>(d_k);
+  pp.v = nullptr;
+  pp.q_norm_weight = reinterpret_cast<const uint16_t *>(d_q_norm_weight);
+  pp.k_norm_weight = reinterpret_cast<const uint16_t *>(d_k_norm_weight);
+  pp.cos = d_cos;
+  pp.sin = d_sin;
+  pp.token_position = d_token_position;
+  // 1x512 geometry: RoPE over a quarter of the head, V from the raw K.
+  hipLaunchKernelGGL((prefill_prep_kernel<1, 512, 128, false>), dim3(batch_size * seqlen_q, 1),
+                     dim3(prep_waves<1, false>() * kWave), 0, stream, pp);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return err;
+  D512Params ap{};
+  ap.out = reinterpret_cast<uint16_t *>(d_out);
+  ap.q = reinterpret_cast<const uint16_t *>(d_q_prepared);
+  ap.k = reinterpret_cast<const uint16_t *>(d_k_prepared);
+  ap.v = reinterpret_cast<const uint16_t *>(d_v_prepared);
+  ap.seq_len = seqlen_q;
+  ap.q_scale = softmax_scale * kLog2e;
+  hipLaunchKernelGGL(prefill_d512_kernel,
+                     dim3((seqlen_q + kD512Rows - 1) / kD512Rows, batch_size),
+                     dim3(kD512Threads), 0, stream, ap);
+  return hipGetLastError();
+}

@@ -81,6 +81,10 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _P]),
     "gemma4_flash_attention_prefill_chunk_paged_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _F32, _P]),
+    "gemma4_flash_attention_sliding_fwd_bf16_norm_rope": (
+        _I32, [_P] * 12 + [_I32, _I32, _I32, _I32, _F32, _P]),
+    "gemma4_flash_attention_global_fwd_bf16_norm_rope": (
+        _I32, [_P] * 11 + [_I32, _I32, _I32, _F32, _P]),
     "gemma4_runtime_create": (_I32, [ctypes.POINTER(_P), _I32, _I32, _I32, _P]),
     "gemma4_runtime_destroy": (None, [_P]),
     "gemma4_runtime_prefill": (_I32, [_P, _I32, _P]),
@@ -351,6 +355,26 @@ class Runtime:
 
     def device_ptr(self, name) -> int:
         return lib().gemma4_runtime_device_ptr(self._h, self.DEVICE[name]) or 0
+
+
+def flash_attention_sliding_fwd_bf16_norm_rope(out, q_prepared, k_prepared, v_prepared, q, k, v,
+                                               q_norm_weight, k_norm_weight, cos, sin,
+                                               token_position, batch_size, seqlen_q, seqlen_k,
+                                               window_size, softmax_scale, stream=None) -> int:
+    return lib().gemma4_flash_attention_sliding_fwd_bf16_norm_rope(
+        ptr(out), ptr(q_prepared), ptr(k_prepared), ptr(v_prepared), ptr(q), ptr(k), ptr(v),
+        ptr(q_norm_weight), ptr(k_norm_weight), ptr(cos), ptr(sin), ptr(token_position),
+        batch_size, seqlen_q, seqlen_k, window_size, softmax_scale, stream_handle(stream))
+
+
+def flash_attention_global_fwd_bf16_norm_rope(out, q_prepared, k_prepared, v_prepared, q, k,
+                                              q_norm_weight, k_norm_weight, cos, sin,
+                                              token_position, batch_size, seqlen_q, seqlen_k,
+                                              softmax_scale, stream=None) -> int:
+    return lib().gemma4_flash_attention_global_fwd_bf16_norm_rope(
+        ptr(out), ptr(q_prepared), ptr(k_prepared), ptr(v_prepared), ptr(q), ptr(k),
+        ptr(q_norm_weight), ptr(k_norm_weight), ptr(cos), ptr(sin), ptr(token_position),
+        batch_size, seqlen_q, seqlen_k, softmax_scale, stream_handle(stream))
 
 
 def flash_attention_prefill_chunk_paged_bf16(out, q, k, v, cache_k, cache_v, page_table,

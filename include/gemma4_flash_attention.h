@@ -112,6 +112,34 @@ hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
     int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
     hipStream_t stream);
 
+// Prefill self-attention with Q/K/V preparation (seqlen_q == seqlen_k, no
+// prior context), same names, argument order and validation as the
+// reference launchers (src/gemma4_flash_attention.cuh:9-45,
+// src/gemma4_flash_attention_prefill.cu:1110-1257). Row r of the
+// [batch_size][seqlen_q] token rows is prepared at absolute position
+// d_token_position[r] (rows with a negative position are not prepared):
+// Q and K get learned RMSNorm then split-half RoPE from d_cos/d_sin
+// ([position][rotary_dim/2]); V gets scale-free RMSNorm. Sliding: 8 kv heads
+// x 256, RoPE over the whole head, V from d_v, causal attention within
+// `window_size` keys (> 0). Global: 1 kv head x 512, RoPE over the first 128
+// dims, V derived from the raw K (d_v does not exist), causal attention.
+// Prepared tensors keep the attention layout: q [rows][16][D], k/v
+// [rows][Hk][D]; out [rows][16][D]. The caller owns all buffers; these
+// entry points have C linkage here (the reference's are C++).
+hipError_t gemma4_flash_attention_sliding_fwd_bf16_norm_rope(
+    gemma4_bf16 *d_out, gemma4_bf16 *d_q_prepared, gemma4_bf16 *d_k_prepared,
+    gemma4_bf16 *d_v_prepared, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_v, const gemma4_bf16 *d_q_norm_weight,
+    const gemma4_bf16 *d_k_norm_weight, const float *d_cos, const float *d_sin,
+    const int32_t *d_token_position, int batch_size, int seqlen_q, int seqlen_k, int window_size,
+    float softmax_scale, hipStream_t stream);
+hipError_t gemma4_flash_attention_global_fwd_bf16_norm_rope(
+    gemma4_bf16 *d_out, gemma4_bf16 *d_q_prepared, gemma4_bf16 *d_k_prepared,
+    gemma4_bf16 *d_v_prepared, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_q_norm_weight, const gemma4_bf16 *d_k_norm_weight, const float *d_cos,
+    const float *d_sin, const int32_t *d_token_position, int batch_size, int seqlen_q,
+    int seqlen_k, float softmax_scale, hipStream_t stream);
+
 // Split plan for the MI355X: the split size (a multiple of the kernel's key
 // wave chunk) that gives about `target_workgroups` split workgroups (0 = default,
 // eight per CU) for `batch_count` sequences of up to `max_live_keys` live keys,
