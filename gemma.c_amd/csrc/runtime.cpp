@@ -72,7 +72,17 @@ hipError_t upload_all(Gemma4RuntimeState *s, size_t tokens, hipStream_t stream) 
   if ((e = upload(s->seq_lengths, s->h_seq_lengths.data(), s->h_seq_lengths.size(),
                   stream)) != hipSuccess) return e;
   if ((e = upload(s->token_batch, s->h_token_batch.data(), tokens, stream)) != hipSuccess) return e;
-  return upload(s->token_position, s->h_token_position.data(), tokens, stream);
+  if ((e = upload(s->token_position, s->h_token_position.data(), tokens, stream)) != hipSuccess) return e;
+  if ((e = upload(s->sliding_slot_logical_pages, s->h_sliding_slot_logical_pages.data(),
+                  s->h_sliding_slot_logical_pages.size(), stream)) != hipSuccess) return e;
+  return upload(s->global_slot_logical_pages, s->h_global_slot_logical_pages.data(),
+                s->h_global_slot_logical_pages.size(), stream);
+}
+
+template <typename T>
+hipError_t download(std::vector<T> &dst, const T *src, size_t count, hipStream_t stream) {
+  if (count == 0) return hipSuccess;
+  return hipMemcpyAsync(dst.data(), src, count * sizeof(T), hipMemcpyDeviceToHost, stream);
 }
 
 }  // namespace
@@ -81,7 +91,8 @@ void gemma4_runtime_state_free(Gemma4RuntimeState *s) {
   void *ptrs[] = {s->sliding_cache_k, s->sliding_cache_v, s->global_cache_k, s->global_cache_v,
                   s->sliding_page_table, s->global_page_table, s->seq_lengths,
                   s->token_batch, s->token_position, s->sliding_cos, s->sliding_sin,
-                  s->global_cos, s->global_sin};
+                  s->global_cos, s->global_sin, s->sliding_slot_logical_pages,
+                  s->global_slot_logical_pages, s->device_step_status};
   for (void *p : ptrs) {
     if (p != nullptr) (void)hipFree(p);
   }
@@ -140,6 +151,10 @@ hipError_t gemma4_runtime_state_init(Gemma4RuntimeState *s, int32_t batch_size,
   step(alloc(&s->sliding_sin, ss.size()));
   step(alloc(&s->global_cos, gc.size()));
   step(alloc(&s->global_sin, gs.size()));
+  step(alloc(&s->sliding_slot_logical_pages, s->h_sliding_slot_logical_pages.size()));
+  step(alloc(&s->global_slot_logical_pages, s->h_global_slot_logical_pages.size()));
+  step(alloc(&s->device_step_status, 1));
+  if (e == hipSuccess) step(hipMemsetAsync(s->device_step_status, 0, sizeof(int32_t), stream));
   if (e == hipSuccess) {
     step(upload(s->sliding_cos, sc.data(), sc.size(), stream));
     step(upload(s->sliding_sin, ss.data(), ss.size(), stream));
@@ -180,11 +195,41 @@ hipError_t gemma4_runtime_prepare_prefill(Gemma4RuntimeState *s, int32_t seq_len
   s->token_count = s->batch_size * seq_len;
   hipError_t e = upload_all(s, (size_t)s->token_count, stream);
   if (e == hipSuccess) e = hipStreamSynchronize(stream);  // host vectors may change next
+  if (e == hipSuccess) s->host_stale = false;  // rebuilt from scratch on the host
   return e;
+}
+
+hipError_t gemma4_runtime_sync_host(Gemma4RuntimeState *s, hipStream_t stream) {
+  if (s == nullptr) return hipErrorInvalidValue;
+  hipError_t e;
+  if ((e = download(s->h_sliding_page_table, s->sliding_page_table,
+                    s->h_sliding_page_table.size(), stream)) != hipSuccess) return e;
+  if ((e = download(s->h_global_page_table, s->global_page_table,
+                    s->h_global_page_table.size(), stream)) != hipSuccess) return e;
+  if ((e = download(s->h_sliding_slot_logical_pages, s->sliding_slot_logical_pages,
+                    s->h_sliding_slot_logical_pages.size(), stream)) != hipSuccess) return e;
+  if ((e = download(s->h_global_slot_logical_pages, s->global_slot_logical_pages,
+                    s->h_global_slot_logical_pages.size(), stream)) != hipSuccess) return e;
+  if ((e = download(s->h_seq_lengths, s->seq_lengths, s->h_seq_lengths.size(), stream)) != hipSuccess) return e;
+  const size_t tokens = (size_t)std::max(s->token_count, 0);
+  if ((e = download(s->h_token_batch, s->token_batch, tokens, stream)) != hipSuccess) return e;
+  if ((e = download(s->h_token_position, s->token_position, tokens, stream)) != hipSuccess) return e;
+  if ((e = hipStreamSynchronize(stream)) != hipSuccess) return e;
+  s->host_stale = false;
+  return hipSuccess;
+}
+
+hipError_t gemma4_runtime_device_step_status(const Gemma4RuntimeState *s, int32_t *status) {
+  if (s == nullptr || status == nullptr || s->device_step_status == nullptr) return hipErrorInvalidValue;
+  return hipMemcpy(status, s->device_step_status, sizeof(int32_t), hipMemcpyDeviceToHost);
 }
 
 hipError_t gemma4_runtime_prepare_decode_step(Gemma4RuntimeState *s, hipStream_t stream) {
   if (s == nullptr) return hipErrorInvalidValue;
+  if (s->host_stale) {  // device-side steps ran since the host vectors were current
+    const hipError_t se = gemma4_runtime_sync_host(s, stream);
+    if (se != hipSuccess) return se;
+  }
   const Gemma4KvCacheConfig &sc = s->sliding_cache_config;
   const Gemma4KvCacheConfig &gc = s->global_cache_config;
   // Validate every sequence before any mutation: the position must fit and
@@ -215,6 +260,10 @@ hipError_t gemma4_runtime_prepare_decode_step(Gemma4RuntimeState *s, hipStream_t
     const size_t gi = (size_t)b * gc.max_pages_per_seq + (pos / gc.page_size) % gc.max_pages_per_seq;
     if (e == hipSuccess) e = upload(s->sliding_page_table + si, &s->h_sliding_page_table[si], 1, stream);
     if (e == hipSuccess) e = upload(s->global_page_table + gi, &s->h_global_page_table[gi], 1, stream);
+    if (e == hipSuccess)
+      e = upload(s->sliding_slot_logical_pages + si, &s->h_sliding_slot_logical_pages[si], 1, stream);
+    if (e == hipSuccess)
+      e = upload(s->global_slot_logical_pages + gi, &s->h_global_slot_logical_pages[gi], 1, stream);
   }
   for (int32_t b = 0; b < s->batch_size; ++b) ++s->h_seq_lengths[b];
   s->token_count = s->batch_size;
@@ -261,6 +310,20 @@ hipError_t gemma4_runtime_prefill(Gemma4Runtime *rt, int32_t seq_len, hipStream_
 hipError_t gemma4_runtime_decode_step(Gemma4Runtime *rt, hipStream_t stream) {
   return rt == nullptr ? hipErrorInvalidValue
                        : gemma4_runtime_prepare_decode_step(&rt->state, stream);
+}
+
+hipError_t gemma4_runtime_decode_step_device(Gemma4Runtime *rt, hipStream_t stream) {
+  return rt == nullptr ? hipErrorInvalidValue
+                       : gemma4_runtime_prepare_decode_step_device(&rt->state, stream);
+}
+
+hipError_t gemma4_runtime_sync_host_state(Gemma4Runtime *rt, hipStream_t stream) {
+  return rt == nullptr ? hipErrorInvalidValue : gemma4_runtime_sync_host(&rt->state, stream);
+}
+
+hipError_t gemma4_runtime_get_device_step_status(const Gemma4Runtime *rt, int32_t *status) {
+  return rt == nullptr ? hipErrorInvalidValue
+                       : gemma4_runtime_device_step_status(&rt->state, status);
 }
 
 hipError_t gemma4_runtime_get_config(const Gemma4Runtime *rt, int32_t which,
@@ -318,7 +381,8 @@ void *gemma4_runtime_device_ptr(const Gemma4Runtime *rt, int32_t which) {
   void *const ptrs[] = {s.sliding_cache_k, s.sliding_cache_v, s.global_cache_k, s.global_cache_v,
                         s.sliding_page_table, s.global_page_table, s.seq_lengths,
                         s.token_batch, s.token_position, s.sliding_cos, s.sliding_sin,
-                        s.global_cos, s.global_sin};
+                        s.global_cos, s.global_sin, s.sliding_slot_logical_pages,
+                        s.global_slot_logical_pages};
   if (which < 0 || which >= (int32_t)(sizeof(ptrs) / sizeof(ptrs[0]))) return nullptr;
   return ptrs[which];
 }

@@ -89,6 +89,9 @@ SIGNATURES = {
     "gemma4_runtime_destroy": (None, [_P]),
     "gemma4_runtime_prefill": (_I32, [_P, _I32, _P]),
     "gemma4_runtime_decode_step": (_I32, [_P, _P]),
+    "gemma4_runtime_decode_step_device": (_I32, [_P, _P]),
+    "gemma4_runtime_sync_host_state": (_I32, [_P, _P]),
+    "gemma4_runtime_get_device_step_status": (_I32, [_P, ctypes.POINTER(_I32)]),
     "gemma4_runtime_get_config": (_I32, [_P, _I32, ctypes.POINTER(_CFG)]),
     "gemma4_runtime_get_scalars": (_I32, [_P, ctypes.POINTER(_I32)]),
     "gemma4_runtime_get_host_vector": (_I32, [_P, _I32, _P, _I64, ctypes.POINTER(_I64)]),
@@ -304,7 +307,8 @@ class Runtime:
     DEVICE = {"sliding_cache_k": 0, "sliding_cache_v": 1, "global_cache_k": 2,
               "global_cache_v": 3, "sliding_page_table": 4, "global_page_table": 5,
               "seq_lengths": 6, "token_batch": 7, "token_position": 8, "sliding_cos": 9,
-              "sliding_sin": 10, "global_cos": 11, "global_sin": 12}
+              "sliding_sin": 10, "global_cos": 11, "global_sin": 12,
+              "sliding_slot_logical_pages": 13, "global_slot_logical_pages": 14}
 
     def __init__(self, batch_size, max_seq_len, page_size, stream=None):
         self._h = ctypes.c_void_p()
@@ -327,6 +331,17 @@ class Runtime:
 
     def prepare_decode_step(self, stream=None) -> int:
         return lib().gemma4_runtime_decode_step(self._h, stream_handle(stream))
+
+    def prepare_decode_step_device(self, stream=None) -> int:
+        return lib().gemma4_runtime_decode_step_device(self._h, stream_handle(stream))
+
+    def sync_host(self, stream=None) -> int:
+        return lib().gemma4_runtime_sync_host_state(self._h, stream_handle(stream))
+
+    def device_step_status(self) -> int:
+        out = _I32()
+        check(lib().gemma4_runtime_get_device_step_status(self._h, ctypes.byref(out)))
+        return out.value
 
     def config(self, global_cache: bool) -> Gemma4KvCacheConfig:
         c = Gemma4KvCacheConfig()

@@ -42,6 +42,14 @@ struct Gemma4RuntimeState {
   std::vector<int32_t> h_seq_lengths;
   std::vector<int32_t> h_token_batch;
   std::vector<int32_t> h_token_position;
+
+  // Extensions of this build (not in the reference struct): device copies of
+  // the ring bookkeeping for the device-side decode step, its status word,
+  // and whether device metadata is ahead of the host vectors.
+  int32_t *sliding_slot_logical_pages = nullptr;
+  int32_t *global_slot_logical_pages = nullptr;
+  int32_t *device_step_status = nullptr;
+  bool host_stale = false;
 };
 
 // Replaces src/gemma4_runtime.cuh:45-64 (src/gemma4_runtime.cu:95-341).
@@ -60,6 +68,23 @@ hipError_t gemma4_runtime_prepare_prefill(Gemma4RuntimeState *state, int32_t seq
 // the changed metadata.
 hipError_t gemma4_runtime_prepare_decode_step(Gemma4RuntimeState *state,
                                               hipStream_t stream);
+// Device-side decode step (no counterpart in the reference; it removes the
+// per-step host bookkeeping and H2D copies, as the reference's TODO.md:7
+// plans): one kernel validates every sequence (position < max_seq_len, no
+// ring slot holding a newer logical page) and, only if all pass, maps the
+// ring slots, writes token_batch/token_position and advances seq_lengths on
+// the device. Stream-ordered and asynchronous: a refused step changes
+// nothing and sets the device status word to 1 (0 after an applied step),
+// read with gemma4_runtime_device_step_status. The host vectors are then
+// stale until gemma4_runtime_sync_host (the host prepare_* functions sync
+// first by themselves).
+hipError_t gemma4_runtime_prepare_decode_step_device(Gemma4RuntimeState *state,
+                                                     hipStream_t stream);
+// Copies the device metadata into the host vectors (synchronous).
+hipError_t gemma4_runtime_sync_host(Gemma4RuntimeState *state, hipStream_t stream);
+// Status of the last device-side step (synchronous read): 0 applied, 1 refused.
+hipError_t gemma4_runtime_device_step_status(const Gemma4RuntimeState *state,
+                                             int32_t *status);
 extern "C" {
 #endif
 
@@ -73,6 +98,11 @@ hipError_t gemma4_runtime_create(Gemma4Runtime **out, int32_t batch_size,
 void gemma4_runtime_destroy(Gemma4Runtime *rt);
 hipError_t gemma4_runtime_prefill(Gemma4Runtime *rt, int32_t seq_len, hipStream_t stream);
 hipError_t gemma4_runtime_decode_step(Gemma4Runtime *rt, hipStream_t stream);
+// Handle forms of the device-side step, the host sync and the status read
+// (no counterparts in the reference; see the C++ functions above).
+hipError_t gemma4_runtime_decode_step_device(Gemma4Runtime *rt, hipStream_t stream);
+hipError_t gemma4_runtime_sync_host_state(Gemma4Runtime *rt, hipStream_t stream);
+hipError_t gemma4_runtime_get_device_step_status(const Gemma4Runtime *rt, int32_t *status);
 // which: 0 sliding config, 1 global config.
 hipError_t gemma4_runtime_get_config(const Gemma4Runtime *rt, int32_t which,
                                      Gemma4KvCacheConfig *out);
@@ -89,7 +119,8 @@ hipError_t gemma4_runtime_set_host_seq_lengths(Gemma4Runtime *rt, const int32_t 
                                                int64_t count);
 // Device pointers: 0 sliding K, 1 sliding V, 2 global K, 3 global V,
 // 4 sliding page table, 5 global page table, 6 seq_lengths, 7 token_batch,
-// 8 token_position, 9 sliding cos, 10 sliding sin, 11 global cos, 12 global sin.
+// 8 token_position, 9 sliding cos, 10 sliding sin, 11 global cos, 12 global sin,
+// 13 sliding slot logical pages, 14 global slot logical pages.
 void *gemma4_runtime_device_ptr(const Gemma4Runtime *rt, int32_t which);
 
 #ifdef __cplusplus

@@ -116,3 +116,63 @@ def test_ring_walk_matches_oracle_bookkeeping(dev):
 def test_init_rejects_bad_sizes(dev):
     for args in [(0, 10, 4), (1, 0, 4), (1, 10, 0), (1, 262145, 64)]:
         assert gk.Runtime(*args).init_code == gk.HIP_ERROR_INVALID_VALUE
+
+
+def _device_state(rt, batch):
+    names = ("sliding_page_table", "global_page_table", "sliding_slot_logical_pages",
+             "global_slot_logical_pages")
+    out = {n: _device_i32(rt.device_ptr(n), rt.host(n).size) for n in names}
+    out["seq_lengths"] = _device_i32(rt.device_ptr("seq_lengths"), batch)
+    out["token_batch"] = _device_i32(rt.device_ptr("token_batch"), batch)
+    out["token_position"] = _device_i32(rt.device_ptr("token_position"), batch)
+    return out
+
+
+def test_device_decode_step_matches_host_step(dev):
+    """The device-side step (one kernel, no host bookkeeping) leaves exactly
+    the device metadata the host step uploads, through a sliding-ring wrap
+    (page 16, 65 slots), mixed with host steps; a refused device step (one
+    step at max_seq_len) changes nothing and reports status 1."""
+    import torch
+    batch, max_seq = 3, 1200
+    host_rt, dev_rt = gk.Runtime(batch, max_seq, 16), gk.Runtime(batch, max_seq, 16)
+    gk.check(host_rt.init_code)
+    gk.check(dev_rt.init_code)
+    gk.check(host_rt.prepare_prefill(1000))
+    gk.check(dev_rt.prepare_prefill(1000))
+    for step in range(120):
+        gk.check(host_rt.prepare_decode_step())
+        if step % 40 == 39:
+            gk.check(dev_rt.prepare_decode_step())  # host step after device steps: syncs first
+        else:
+            gk.check(dev_rt.prepare_decode_step_device())
+        if step % 20 == 0 or step == 119:
+            torch.cuda.synchronize()
+            a, b = _device_state(host_rt, batch), _device_state(dev_rt, batch)
+            for k in a:
+                assert np.array_equal(a[k], b[k]), (step, k)
+            assert dev_rt.device_step_status() == 0
+    gk.check(dev_rt.sync_host())
+    for k in gk.Runtime.HOST:
+        if k in ("token_batch", "token_position"):
+            assert np.array_equal(dev_rt.host(k)[:batch], host_rt.host(k)[:batch]), k
+        else:
+            assert np.array_equal(dev_rt.host(k), host_rt.host(k)), k
+    # Refusal: sequence 1 at max_seq_len. Nothing changes, status 1.
+    gk.check(dev_rt.prepare_prefill(max_seq - 5))  # rebuild, then walk up to max_seq_len
+    for _ in range(5):
+        gk.check(dev_rt.prepare_decode_step_device())
+    torch.cuda.synchronize()
+    assert dev_rt.device_step_status() == 0
+    before = _device_state(dev_rt, batch)
+    assert list(before["seq_lengths"]) == [max_seq] * batch
+    gk.check(dev_rt.prepare_decode_step_device())
+    torch.cuda.synchronize()
+    assert dev_rt.device_step_status() == 1
+    after = _device_state(dev_rt, batch)
+    for k in before:
+        assert np.array_equal(before[k], after[k]), k
+    # The host form refuses the same step once it has synced.
+    assert dev_rt.prepare_decode_step() == gk.HIP_ERROR_INVALID_VALUE
+    host_rt.close()
+    dev_rt.close()
