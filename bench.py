@@ -216,7 +216,9 @@ def bench_prefill(torch, gk, dev, reps):
         # Back-to-back eager launches: each chunk is long enough that the
         # launch cost hides behind the previous one (a graph replay per
         # launch would add its own overhead to every chunk).
-        ms = time_eager(torch, fn, max(reps, 30), 10)
+        # ~50 warm-up launches: the first tens of milliseconds of a fresh
+        # process run several percent slower (clock ramp).
+        ms = time_eager(torch, fn, max(reps, 50), 50)
         keys = np.arange(lq) + prior + 1
         if window:
             keys = np.minimum(keys, window)

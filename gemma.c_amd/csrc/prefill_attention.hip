@@ -179,6 +179,7 @@ __device__ __forceinline__ void copy_row_pair(uint64_t src, uint32_t lds_addr) {
   asm volatile(
       "s_mov_b32 %[m0s], m0\n\t"
       "s_mov_b32 m0, %[lds]\n\t"
+      "s_nop 0\n\t"  // SALU write of M0 -> LDS DMA reading it: one wait state (gfx9)
       "global_load_lds_dwordx4 %[src], off\n\t"
       "s_mov_b32 m0, %[m0s]"
       : [m0s] "=&s"(m0_saved)
@@ -193,6 +194,7 @@ __device__ __forceinline__ void copy_dwords(const void *src, uint32_t lds_addr) 
   asm volatile(
       "s_mov_b32 %[m0s], m0\n\t"
       "s_mov_b32 m0, %[lds]\n\t"
+      "s_nop 0\n\t"  // SALU write of M0 -> LDS DMA reading it: one wait state (gfx9)
       "global_load_lds_dword %[src], off\n\t"
       "s_mov_b32 m0, %[m0s]"
       : [m0s] "=&s"(m0_saved)
