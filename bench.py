@@ -320,6 +320,105 @@ def bench_batch64(torch, gk, dev, steps, warmup):
             "bytes_per_step": total}
 
 
+def bench_widened(torch, gk, dev):
+    """The rows around the hot path, each timed on its own: the decode-token
+    prep + append (both geometries, batch 1 and 64), the prefill norm+RoPE
+    launchers (prep + attention, 2048 rows), and the runtime's decode-step
+    bookkeeping on the host vs on the device. Synthetic N(0,1) inputs."""
+    import time as _time
+    import numpy as np
+    res = {}
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=gen, device=dev).bfloat16().view(torch.int16)
+
+    # Decode prep + append: one token per sequence into a paged cache.
+    prep = {}
+    for name, heads, dim, rot, theta in (("sliding_8x256", 8, 256, 256, 10000.0),
+                                         ("global_1x512", 1, 512, 128, 1_000_000.0)):
+        for batch in (1, 64):
+            page, max_pages = 16, 64
+            cfg = gk.make_config(1, batch * max_pages, page, max_pages, batch, heads, dim,
+                                 0 if heads == 1 else 1024)
+            ck = torch.zeros((batch * max_pages * page, heads, dim), dtype=torch.int16, device=dev)
+            cv = torch.zeros_like(ck)
+            pt = torch.arange(batch * max_pages, dtype=torch.int32, device=dev)
+            pos = torch.full((batch,), 100, dtype=torch.int32, device=dev)
+            q, k, v = rnd((batch, QH, dim)), rnd((batch, heads, dim)), rnd((batch, heads, dim))
+            qp = torch.empty_like(q)
+            w = rnd((dim,))
+            cos = torch.rand((1024, rot // 2), device=dev)
+            sin = torch.rand((1024, rot // 2), device=dev)
+
+            def fn(st):
+                gk.check(gk.decode_prep_append_bf16(qp, ck, cv, cfg, pt, pos, 0, q, k,
+                                                    v if heads > 1 else None, w, w, cos, sin,
+                                                    batch, stream=st), "decode prep")
+            us = time_each(torch, fn, 50) * 1e3
+            nbytes = batch * (2 * QH * dim * 2 + 4 * heads * dim * 2)  # q in/out, k,v in, cache rows out
+            prep[f"{name}_batch{batch}"] = {"us": round(us, 2),
+                                            "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    res["decode_prep_append"] = prep
+
+    # Prefill launchers: prep + causal attention over 2048 rows.
+    lq = 2048
+    launch = {}
+    for name in ("sliding_8x256_window1024", "global_1x512"):
+        heads, dim, rot = (8, 256, 256) if name.startswith("sliding") else (1, 512, 128)
+        q, k, v = rnd((lq, QH, dim)), rnd((lq, heads, dim)), rnd((lq, heads, dim))
+        qp, kp, vp, out = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(q)
+        w = rnd((dim,))
+        cos = torch.rand((lq, rot // 2), device=dev)
+        sin = torch.rand((lq, rot // 2), device=dev)
+        pos = torch.arange(lq, dtype=torch.int32, device=dev)
+        scale = 1 / math.sqrt(dim)
+        if heads == 8:
+            def fn(st):
+                gk.check(gk.flash_attention_sliding_fwd_bf16_norm_rope(
+                    out, qp, kp, vp, q, k, v, w, w, cos, sin, pos, 1, lq, lq, 1024, scale,
+                    stream=st), "sliding launcher")
+            keys = np.minimum(np.arange(lq) + 1, 1024)
+        else:
+            def fn(st):
+                gk.check(gk.flash_attention_global_fwd_bf16_norm_rope(
+                    out, qp, kp, vp, q, k, w, w, cos, sin, pos, 1, lq, lq, scale, stream=st),
+                    "global launcher")
+            keys = np.arange(lq) + 1
+        ms = time_eager(torch, fn, 20, 5)
+        flops = 4 * dim * QH * int(keys.sum())
+        launch[name] = {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
+    res["prefill_norm_rope_launchers"] = launch
+
+    # Runtime decode-step bookkeeping: host (validate, map, H2D copies) vs
+    # device (one kernel), wall time per step with the stream drained.
+    rt_res = {}
+    for batch in (1, 64):
+        rt_h, rt_d = gk.Runtime(batch, 1100, 16), gk.Runtime(batch, 1100, 16)
+        gk.check(rt_h.init_code)
+        gk.check(rt_d.init_code)
+        gk.check(rt_h.prepare_prefill(900))
+        gk.check(rt_d.prepare_prefill(900))
+        torch.cuda.synchronize()
+        t0 = _time.perf_counter()
+        for _ in range(100):
+            gk.check(rt_h.prepare_decode_step())
+        torch.cuda.synchronize()
+        t1 = _time.perf_counter()
+        for _ in range(100):
+            gk.check(rt_d.prepare_decode_step_device())
+        torch.cuda.synchronize()
+        t2 = _time.perf_counter()
+        assert rt_d.device_step_status() == 0
+        rt_res[f"batch{batch}"] = {"host_us": round((t1 - t0) * 1e4, 1),
+                                   "device_us": round((t2 - t1) * 1e4, 1)}
+        rt_h.close()
+        rt_d.close()
+    res["runtime_decode_step"] = rt_res
+    return res
+
+
 def cpu_baseline(max_seconds: float):
     """BASELINE config 1 on the host with the C oracle (1 thread): single
     sliding layer, 8x256 KV, 16 q heads, 1024-slot ring (page 1), sequential
@@ -378,7 +477,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch64", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill"],
+    ap.add_argument("--no-widened", action="store_true")
+    ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill",
+                                       "widened"],
                     default=None,
                     help="profiling helper: run one leg only")
     args = ap.parse_args()
@@ -405,6 +506,9 @@ def main():
 
     if args.only == "prefill":
         print(json.dumps(bench_prefill(torch, gk, dev, args.steps)))
+        return
+    if args.only == "widened":
+        print(json.dumps(bench_widened(torch, gk, dev)))
         return
 
     layers, caches, meta, scratch = build_config2(torch, gk, dev)
@@ -519,6 +623,8 @@ def main():
     del caches, runner
     if not args.no_prefill:
         result["prefill_config5"] = bench_prefill(torch, gk, dev, max(5, args.steps // 2))
+    if not args.no_widened:
+        result["widened"] = bench_widened(torch, gk, dev)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(result))
