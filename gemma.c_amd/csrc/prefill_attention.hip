@@ -48,6 +48,7 @@
 // sees skip the mask. Blocks are ordered head-fastest so the workgroups of
 // one kv head land on one XCD and share its L2 as they stream the same keys.
 #include "gemma4_device.hpp"
+#include "lds_copy.hpp"
 
 #include "gemma4_flash_attention.h"
 
@@ -168,45 +169,6 @@ __device__ __forceinline__ void read_kfrags(uint32_t k_addr, u32x4v_t (&kf)[16])
 template <int kStep>
 __device__ __forceinline__ void kfrag_ready(u32x4v_t &f) {
   asm volatile("s_waitcnt lgkmcnt(%[n])" : "+a"(f) : [n] "i"(15 - kStep));
-}
-
-// One 1 KiB LDS copy (global_load_lds, 16 bytes per lane): LDS bytes
-// [lds_addr, +1024) from the per-lane addresses src. The copy is invisible
-// to the compiler's memory counters: the caller waits for it (vmcnt) before
-// the barrier that publishes the tile.
-__device__ __forceinline__ void copy_row_pair(uint64_t src, uint32_t lds_addr) {
-  uint32_t m0_saved;
-  asm volatile(
-      "s_mov_b32 %[m0s], m0\n\t"
-      "s_mov_b32 m0, %[lds]\n\t"
-      "s_nop 0\n\t"  // SALU write of M0 -> LDS DMA reading it: one wait state (gfx9)
-      "global_load_lds_dwordx4 %[src], off\n\t"
-      "s_mov_b32 m0, %[m0s]"
-      : [m0s] "=&s"(m0_saved)
-      : [lds] "s"(lds_addr), [src] "v"(src));
-}
-
-// One 4-byte-per-lane LDS copy: LDS bytes [lds_addr, +256) from the
-// per-lane addresses src (global_load_lds_dword); waited for like
-// copy_row_pair.
-__device__ __forceinline__ void copy_dwords(const void *src, uint32_t lds_addr) {
-  uint32_t m0_saved;
-  asm volatile(
-      "s_mov_b32 %[m0s], m0\n\t"
-      "s_mov_b32 m0, %[lds]\n\t"
-      "s_nop 0\n\t"  // SALU write of M0 -> LDS DMA reading it: one wait state (gfx9)
-      "global_load_lds_dword %[src], off\n\t"
-      "s_mov_b32 m0, %[m0s]"
-      : [m0s] "=&s"(m0_saved)
-      : [lds] "s"(lds_addr), [src] "v"(src));
-}
-
-// Waits for every vector memory operation of this wave, the copies
-// included (s_waitcnt vmcnt(0); a builtin rather than inline asm so the
-// compiler's own counter bookkeeping sees it as well).
-__device__ __forceinline__ void wait_copies() {
-  constexpr int kVmcnt0 = 0x0F70;  // gfx9 encoding: vmcnt 0, expcnt 7, lgkmcnt 15 (no wait)
-  __builtin_amdgcn_s_waitcnt(kVmcnt0);
 }
 
 // f(integral_constant<int, I>) for I = kBegin .. kEnd-1, unrolled.

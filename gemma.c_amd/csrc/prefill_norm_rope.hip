@@ -20,13 +20,15 @@
 // contraction order is permuted to {4g..4g+3, 16+4g..16+4g+3} for lane
 // group g, and V^T is read in that order by two ds_read_b64_tr_b16 per
 // operand. O^T is 128 fp32 per lane, Q^T 64 registers. A workgroup is four
-// consecutive rows that share 32-key K/V tiles staged in LDS (K chunk c of
-// key k at c ^ (k & 15), V chunk c at c ^ ((k & 7) << 1), 16-byte chunks,
-// so the operand reads are bank-conflict free). The lazy online softmax of
+// consecutive rows that share 32-key K/V tiles copied into two LDS stages
+// with global_load_lds (tile t+1 in flight while tile t is computed; K chunk
+// c of key k at c ^ (k & 15), V chunk c at c ^ ((k & 7) << 1), 16-byte
+// chunks, so the operand reads are bank-conflict free). The lazy online softmax of
 // the chunk kernel (maximum moved only when it grows by more than 8 in
 // log2 units). This geometry is outside the BASELINE configs; the kernel is
 // written for parity, not tuned.
 #include "gemma4_device.hpp"
+#include "lds_copy.hpp"
 #include "prep_common.hpp"
 
 #include "gemma4_flash_attention.h"
@@ -116,8 +118,12 @@ __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
 __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Params p) {
   constexpr int KS = kD512 / 32;  // 32-dim k-steps of S^T
   constexpr int DB = kD512 / 16;  // 16-dim blocks of O^T
-  __shared__ uint4 s_k[kD512Tile * kD512Chunks];
-  __shared__ uint4 s_v[kD512Tile * kD512Chunks];
+  // Two stages of K and V tiles (32 keys x 1 KiB each).
+  struct Lds {
+    uint4 k[2][kD512Tile * kD512Chunks];
+    uint4 v[2][kD512Tile * kD512Chunks];
+  };
+  __shared__ __attribute__((aligned(1024))) Lds lds;
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -148,22 +154,34 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
   const uint16_t *kseq = p.k + (int64_t)b * L * kD512;
   const uint16_t *vseq = p.v + (int64_t)b * L * kD512;
   const int n_tiles = last_key / kD512Tile + 1;
+  // Copy of a tile into a stage: wave w copies keys 8w .. 8w+7, one 1 KiB
+  // row per copy; lane l fills LDS chunk l with the swizzled source chunk.
+  constexpr int kCopyRows = kD512Tile / (kD512Threads / kWave);
+  auto copy_tile = [&](int kt, int stage) {
+#pragma unroll
+    for (int i = 0; i < kCopyRows; ++i) {
+      const int key = kCopyRows * wave + i;
+      const int64_t src_row = (int64_t)min(kt + key, L - 1) * kD512;  // past the end: masked
+      const uint32_t dk = lds_address(&lds.k[stage][key * kD512Chunks]);
+      const uint32_t dv = lds_address(&lds.v[stage][key * kD512Chunks]);
+      copy_row_pair(reinterpret_cast<uint64_t>(kseq + src_row + 8 * (lane ^ (key & 15))),
+                    wave_uniform(dk));
+      copy_row_pair(reinterpret_cast<uint64_t>(vseq + src_row + 8 * (lane ^ ((key & 7) << 1))),
+                    wave_uniform(dv));
+    }
+  };
+  copy_tile(0, 0);
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int kt = tile * kD512Tile;
-    // Stage the tile: thread t copies chunk t % 64 of keys t/64 + 4i.
+    const int stage = tile & 1;
+    // Tile `tile` copied (each wave waits for its own copies, the barrier for
+    // all); every wave is done with tile-1, so the other stage is free.
+    wait_copies();
     __syncthreads();
-#pragma unroll
-    for (int i = 0; i < kD512Tile * kD512Chunks / kD512Threads; ++i) {
-      const int key = t / kD512Chunks + (kD512Threads / kD512Chunks) * i;
-      const int c = t % kD512Chunks;
-      const int src_key = min(kt + key, L - 1);  // past the end: any row, masked below
-      const uint4 kv = load128(kseq + (int64_t)src_key * kD512 + c * 8);
-      const uint4 vv = load128(vseq + (int64_t)src_key * kD512 + c * 8);
-      s_k[key * kD512Chunks + (c ^ (key & 15))] = kv;
-      s_v[key * kD512Chunks + (c ^ ((key & 7) << 1))] = vv;
-    }
-    __syncthreads();
-    if (!row_ok || kt > row) continue;  // uniform per wave; the barriers are at the loop top
+    if (tile + 1 < n_tiles) copy_tile(kt + kD512Tile, stage ^ 1);
+    if (!row_ok || kt > row) continue;  // uniform per wave
+    const uint4 *s_k = lds.k[stage];
+    const uint4 *s_v = lds.v[stage];
 
     // Scores of the two 16-key blocks: lane holds head `head`, keys
     // 16 blk + 4 g + i.
@@ -232,6 +250,8 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
                       acc[d]);
     }
   }
+
+  wait_copies();  // no copy may still be writing LDS when the workgroup exits
 
   // Normalise and store: lane holds head `head`, dims 16 d + 4 g + i.
   l_run += lane_xor<16>(l_run);
