@@ -7,12 +7,11 @@
 // src/gemma4_rope.cu:8-20, src/gemma4_rmsnorm.cu:90-101).
 //
 // Workgroup (kv_head, sequence); one wave per prepared head: the G query
-// heads of the kv head, then K, then V (sliding geometry only). A wave
-// holds its head lane-strided (lane owns dims lane + 64 i), so each
-// rotary pair (d, d + rotary_dim/2) sits in one lane and a head's sum of
-// squares is one wave reduction. The data per token is a few KiB, so the
-// kernel is latency bound; it exists to feed the decode attention kernels
-// prepared q rows and cache rows.
+// heads of the kv head, then K, then V (sliding geometry only); the
+// per-head arithmetic is shared with the prefill prep (prep_common.hpp).
+// The data per token is a few KiB, so the kernel is latency bound; it
+// exists to feed the decode attention kernels prepared q rows and cache
+// rows.
 #include "gemma4_device.hpp"
 #include "decode_common.hpp"
 #include "prep_common.hpp"
@@ -46,7 +45,6 @@ __global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void decode_
     PrepParams p) {
   constexpr int kGroup = kQueryHeads / kHeads;
   constexpr int kPer = kDim / kWave;
-  static_assert(kDim % kWave == 0 && (kRotary / 2) % kWave == 0, "lane-strided pairs");
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = wave_uniform(threadIdx.x / kWave);
   const int32_t head = blockIdx.x;

@@ -56,39 +56,61 @@ struct PrefillPrepParams {
   const int32_t *token_position;  // [rows]
 };
 
-// Workgroup (token row, kv head), one wave per prepared head; a negative
+// Workgroup (block of kPrepRows token rows, kv head), one wave per prepared
+// head; a wave first loads its head of all kPrepRows rows, then prepares
+// and stores them one by one, so the row loads overlap. A negative
 // position skips the row (src/gemma4_flash_attention_prefill.cu:1049-1051).
+constexpr int kPrepRows = 8;
+
 template <int kHeads, int kDim, int kRotary, bool kHasV>
 __global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void prefill_prep_kernel(
-    PrefillPrepParams p) {
+    PrefillPrepParams p, int64_t rows) {
   constexpr int kGroup = kQueryHeads / kHeads;
   constexpr int kPer = kDim / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = wave_uniform(threadIdx.x / kWave);
-  const int64_t row = blockIdx.x;
   const int head = blockIdx.y;
-  const int32_t position = wave_uniform(p.token_position[row]);
-  if (position < 0) return;
-  const float *cos_row = p.cos + (int64_t)position * (kRotary / 2);
-  const float *sin_row = p.sin + (int64_t)position * (kRotary / 2);
-  float x[kPer];
+  const int64_t row0 = (int64_t)blockIdx.x * kPrepRows;
+  int32_t position[kPrepRows];
+#pragma unroll
+  for (int r = 0; r < kPrepRows; ++r)
+    position[r] = row0 + r < rows ? wave_uniform(p.token_position[row0 + r]) : -1;
+  float x[kPrepRows][kPer];
+  // Loads the given tensor's head of every row of the block.
+  auto load_rows = [&](const uint16_t *base, int heads_per_row, int h) {
+#pragma unroll
+    for (int r = 0; r < kPrepRows; ++r) {
+      const int64_t rr = row0 + r < rows ? row0 + r : row0;
+      load_head<kDim>(base + (rr * heads_per_row + h) * kDim, x[r], lane);
+    }
+  };
   if (wave < kGroup) {
-    const int64_t off = (row * kQueryHeads + head * kGroup + wave) * kDim;
-    load_head<kDim>(p.q + off, x, lane);
-    store_weighted_rope<kDim, kRotary>(p.q_prepared + off, x, p.q_norm_weight, cos_row, sin_row,
-                                       lane);
+    const int qh = head * kGroup + wave;
+    load_rows(p.q, kQueryHeads, qh);
+#pragma unroll
+    for (int r = 0; r < kPrepRows; ++r) {
+      if (position[r] < 0) continue;
+      store_weighted_rope<kDim, kRotary>(
+          p.q_prepared + ((row0 + r) * kQueryHeads + qh) * kDim, x[r], p.q_norm_weight,
+          p.cos + (int64_t)position[r] * (kRotary / 2), p.sin + (int64_t)position[r] * (kRotary / 2),
+          lane);
+    }
     if (kHasV || wave != 0) return;
   }
-  const int64_t off = (row * kHeads + head) * kDim;
   const bool k_wave = kHasV ? wave == kGroup : wave == 0;
-  if (k_wave) {
-    load_head<kDim>(p.k + off, x, lane);
-    store_weighted_rope<kDim, kRotary>(p.k_prepared + off, x, p.k_norm_weight, cos_row, sin_row,
-                                       lane);
-    if constexpr (!kHasV) store_scale_free<kDim>(p.v_prepared + off, x, lane);
-  } else {
-    load_head<kDim>(p.v + off, x, lane);
-    store_scale_free<kDim>(p.v_prepared + off, x, lane);
+  load_rows(k_wave ? p.k : p.v, kHeads, head);
+#pragma unroll
+  for (int r = 0; r < kPrepRows; ++r) {
+    if (position[r] < 0) continue;
+    const int64_t off = ((row0 + r) * kHeads + head) * kDim;
+    if (k_wave) {
+      store_weighted_rope<kDim, kRotary>(p.k_prepared + off, x[r], p.k_norm_weight,
+                                         p.cos + (int64_t)position[r] * (kRotary / 2),
+                                         p.sin + (int64_t)position[r] * (kRotary / 2), lane);
+      if constexpr (!kHasV) store_scale_free<kDim>(p.v_prepared + off, x[r], lane);
+    } else {
+      store_scale_free<kDim>(p.v_prepared + off, x[r], lane);
+    }
   }
 }
 
@@ -308,9 +330,10 @@ extern "C" hipError_t gemma4_flash_attention_sliding_fwd_bf16_norm_rope(
   pp.sin = d_sin;
   pp.token_position = d_token_position;
   // 8x256 geometry: RoPE over the whole head, V projection present.
+  const int64_t rows = (int64_t)batch_size * seqlen_q;
   hipLaunchKernelGGL((prefill_prep_kernel<8, 256, 256, true>),
-                     dim3(batch_size * seqlen_q, 8), dim3(prep_waves<8, true>() * kWave), 0,
-                     stream, pp);
+                     dim3((rows + kPrepRows - 1) / kPrepRows, 8),
+                     dim3(prep_waves<8, true>() * kWave), 0, stream, pp, rows);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   // Attention over the prepared rows: the chunk kernel without a prior
@@ -350,8 +373,10 @@ extern "C" hipError_t gemma4_flash_attention_global_fwd_bf16_norm_rope(
   pp.sin = d_sin;
   pp.token_position = d_token_position;
   // 1x512 geometry: RoPE over a quarter of the head, V from the raw K.
-  hipLaunchKernelGGL((prefill_prep_kernel<1, 512, 128, false>), dim3(batch_size * seqlen_q, 1),
-                     dim3(prep_waves<1, false>() * kWave), 0, stream, pp);
+  const int64_t rows = (int64_t)batch_size * seqlen_q;
+  hipLaunchKernelGGL((prefill_prep_kernel<1, 512, 128, false>),
+                     dim3((rows + kPrepRows - 1) / kPrepRows, 1),
+                     dim3(prep_waves<1, false>() * kWave), 0, stream, pp, rows);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return err;
   D512Params ap{};

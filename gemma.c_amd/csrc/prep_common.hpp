@@ -1,9 +1,7 @@
 // Per-head preparation shared by the decode-token and prefill prep kernels
 // (gfx950): learned RMSNorm + split-half RoPE (Q, K) and scale-free RMSNorm
-// (V), one wave per head. A wave holds its head lane-strided (lane owns dims
-// lane + 64 i), so each rotary pair (d, d + rotary_dim/2) sits in one lane
-// and a head's sum of squares is one wave reduction. Follows
-// src/gemma4_flash_attention_decode.cu:216-283,
+// (V), one wave per head; a head's sum of squares is one wave reduction.
+// Follows src/gemma4_flash_attention_decode.cu:216-283,
 // src/gemma4_flash_attention_prefill.cu:960-1021, src/gemma4_rope.cu:8-20 and
 // src/gemma4_rmsnorm.cu:90-101.
 #pragma once
@@ -30,11 +28,44 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// Loads one head lane-strided as fp32.
+// A wave holds a head in contiguous runs: lane l owns dims
+// [l * kPer, (l + 1) * kPer), kPer = D / 64, loaded and stored as one
+// vector. A rotary pair (d, d + R/2) then sits in lanes l and
+// l + (R/2) / kPer, one cross-lane exchange apart.
+template <int kDim>
+struct HeadLayout {
+  static constexpr int kPer = kDim / kWave;
+  static_assert(kPer == 4 || kPer == 8, "4 or 8 bf16 per lane");
+};
+
+// Loads kPer consecutive bf16 as fp32.
+template <int kPer>
+__device__ __forceinline__ void load_run(const uint16_t *src, float (&x)[kPer]) {
+  if constexpr (kPer == 4) {
+    const uint2 w = *reinterpret_cast<const uint2 *>(src);
+    x[0] = bf16_lo(w.x); x[1] = bf16_hi(w.x); x[2] = bf16_lo(w.y); x[3] = bf16_hi(w.y);
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4 *>(src);
+    unpack8(w, x);
+  }
+}
+
+template <int kPer>
+__device__ __forceinline__ void store_run(uint16_t *dst, const float (&y)[kPer]) {
+  if constexpr (kPer == 4) {
+    *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+  } else {
+    *reinterpret_cast<uint4 *>(dst) =
+        make_uint4(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                   pack_bf16x2(y[6], y[7]));
+  }
+}
+
+// Loads one head (this lane's run) as fp32.
 template <int kDim>
 __device__ __forceinline__ void load_head(const uint16_t *src, float (&x)[kDim / kWave], int lane) {
-#pragma unroll
-  for (int i = 0; i < kDim / kWave; ++i) x[i] = bf16_bits_to_f32(src[lane + i * kWave]);
+  constexpr int kPer = HeadLayout<kDim>::kPer;
+  load_run<kPer>(src + lane * kPer, x);
 }
 
 // rsqrt(mean(x^2) + eps) of one head (src/gemma4_rmsnorm.cu:90-101).
@@ -53,39 +84,46 @@ template <int kDim, int kRotary>
 __device__ __forceinline__ void store_weighted_rope(uint16_t *out, const float (&x)[kDim / kWave],
                                                     const uint16_t *weight, const float *cos_row,
                                                     const float *sin_row, int lane) {
-  constexpr int kPer = kDim / kWave;
+  constexpr int kPer = HeadLayout<kDim>::kPer;
   constexpr int kHalf = kRotary / 2;
-  constexpr int kPairSteps = kHalf / kWave;  // lane-strided steps inside the first half
-  static_assert(kDim % kWave == 0 && kHalf % kWave == 0, "lane-strided pairs");
+  constexpr int kPartner = kHalf / kPer;  // lane distance of a rotary pair
+  static_assert(kHalf % kPer == 0 && kPartner < kWave, "pairs in whole lanes");
   const float scale = head_rms_scale<kDim>(x);
+  const int d0 = lane * kPer;
+  float wv[kPer];
+  load_run<kPer>(weight + d0, wv);
   float y[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) y[i] = x[i] * scale * bf16_bits_to_f32(weight[lane + i * kWave]);
+  for (int i = 0; i < kPer; ++i) y[i] = x[i] * scale * wv[i];
+  float partner[kPer];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int d = lane + i * kWave;
-    float r;
-    if (i < kPairSteps) {  // d in the first rotary half
-      const float c = cos_row[d], s = sin_row[d];
-      r = fmaf(-y[i + kPairSteps], s, y[i] * c);
-    } else if (i < 2 * kPairSteps) {  // d in the second rotary half
-      const float c = cos_row[d - kHalf], s = sin_row[d - kHalf];
-      r = fmaf(y[i - kPairSteps], s, y[i] * c);
-    } else {
-      r = y[i];
+  for (int i = 0; i < kPer; ++i) partner[i] = lane_xor<kPartner>(y[i]);
+  float r[kPer];
+  if (d0 < kRotary) {
+    const int pair = d0 < kHalf ? d0 : d0 - kHalf;
+    const float sign = d0 < kHalf ? -1.0f : 1.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const float c = cos_row[pair + i], s = sin_row[pair + i];
+      r[i] = fmaf(sign * partner[i], s, y[i] * c);
     }
-    out[d] = (uint16_t)f32_to_bf16_bits(r);
+  } else {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) r[i] = y[i];
   }
+  store_run<kPer>(out + d0, r);
 }
 
 // Scale-free RMSNorm (src/gemma4_flash_attention_decode.cu:271-283).
 template <int kDim>
 __device__ __forceinline__ void store_scale_free(uint16_t *out, const float (&x)[kDim / kWave],
                                                  int lane) {
+  constexpr int kPer = HeadLayout<kDim>::kPer;
   const float scale = head_rms_scale<kDim>(x);
+  float y[kPer];
 #pragma unroll
-  for (int i = 0; i < kDim / kWave; ++i)
-    out[lane + i * kWave] = (uint16_t)f32_to_bf16_bits(x[i] * scale);
+  for (int i = 0; i < kPer; ++i) y[i] = x[i] * scale;
+  store_run<kPer>(out + lane * kPer, y);
 }
 
 // Waves per workgroup of a prep kernel over one (token, kv head): the query
