@@ -37,6 +37,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 NUM_LAYERS = 48
 HEADS, DIM, QH = 8, 256, 16
+HIDDEN = 3840  # gemma4 hidden width (reference src/gemma4.h:6)
 CONTEXT = 8192
 WINDOW = 1024
 GLOBAL_PAGE = 64
@@ -390,6 +391,33 @@ def bench_widened(torch, gk, dev):
         flops = 4 * dim * QH * int(keys.sum())
         launch[name] = {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
     res["prefill_norm_rope_launchers"] = launch
+
+    # Attention output projection + post-attention norm + residual. The
+    # weights rotate over copies that together exceed the 256 MiB MALL, so
+    # every launch streams its weights from HBM.
+    oproj = {}
+    for width in (4096, 8192):
+        wbytes = HIDDEN * width * 2
+        copies = max(2, -(-384 * 2**20 // wbytes))
+        ws = [rnd((HIDDEN, width)) for _ in range(copies)]
+        g = rnd((HIDDEN,))
+        for rows in (1, 8, 64):
+            attn, x = rnd((rows, width)), rnd((rows, HIDDEN))
+            outs = [torch.empty((rows, HIDDEN), dtype=torch.int16, device=dev) for _ in range(3)]
+            turn = [0]
+
+            def fn(st):
+                w = ws[turn[0] % copies]
+                turn[0] += 1
+                gk.check(gk.attention_o_projection_post_norm_bf16(*outs, attn, w, g, x, rows, width,
+                                                                  stream=st), "o projection")
+            fn(torch.cuda.current_stream().cuda_stream)
+            us = time_each(torch, fn, 60) * 1e3
+            nbytes = wbytes + rows * (width + 4 * HIDDEN) * 2
+            oproj[f"width{width}_rows{rows}"] = {"us": round(us, 2),
+                                                 "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        del ws
+    res["attention_o_projection"] = oproj
 
     # Runtime decode-step bookkeeping: host (validate, map, H2D copies) vs
     # device (one kernel), wall time per step with the stream drained.

@@ -85,6 +85,7 @@ SIGNATURES = {
         _I32, [_P] * 12 + [_I32, _I32, _I32, _I32, _F32, _P]),
     "gemma4_flash_attention_global_fwd_bf16_norm_rope": (
         _I32, [_P] * 11 + [_I32, _I32, _I32, _F32, _P]),
+    "gemma4_attention_o_projection_post_norm_bf16": (_I32, [_P] * 7 + [_I32, _I32, _P]),
     "gemma4_runtime_create": (_I32, [ctypes.POINTER(_P), _I32, _I32, _I32, _P]),
     "gemma4_runtime_destroy": (None, [_P]),
     "gemma4_runtime_prefill": (_I32, [_P, _I32, _P]),
@@ -390,6 +391,15 @@ def flash_attention_global_fwd_bf16_norm_rope(out, q_prepared, k_prepared, v_pre
         ptr(out), ptr(q_prepared), ptr(k_prepared), ptr(v_prepared), ptr(q), ptr(k),
         ptr(q_norm_weight), ptr(k_norm_weight), ptr(cos), ptr(sin), ptr(token_position),
         batch_size, seqlen_q, seqlen_k, softmax_scale, stream_handle(stream))
+
+
+def attention_o_projection_post_norm_bf16(residual_out, normed_out, ffn_residual, attention_out,
+                                          o_proj_col_major, post_norm_weight, attention_x, rows,
+                                          attention_width, stream=None) -> int:
+    return lib().gemma4_attention_o_projection_post_norm_bf16(
+        ptr(residual_out), ptr(normed_out), ptr(ffn_residual), ptr(attention_out),
+        ptr(o_proj_col_major), ptr(post_norm_weight), ptr(attention_x), rows, attention_width,
+        stream_handle(stream))
 
 
 def flash_attention_prefill_chunk_paged_bf16(out, q, k, v, cache_k, cache_v, page_table,

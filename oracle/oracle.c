@@ -471,3 +471,42 @@ void oracle_fill_rope_tables(float *cos_table, float *sin_table,
     }
   }
 }
+
+/* Attention output projection with the post-attention tail, per token row
+ * (src/gemma4_flash_attention_decode.cu:34-129): residual_out[c] =
+ * bf16(sum_e attn[e] * W[c][e]) with W stored column-major
+ * ([hidden][attention_width]); normed_out = bf16(residual * s * weight),
+ * s = rsqrt(mean(residual^2) + eps) over the bf16 residual row
+ * (src/gemma4_rmsnorm.cu:28-85); ffn_residual = bf16(x + normed)
+ * (src/gemma4_cuda_utils.cuh:105-122). Products are summed in float64 here,
+ * so the reference's and the GPU's fp32 summation orders both sit within
+ * rounding of this value. */
+void oracle_attention_o_projection(uint16_t *residual_out, uint16_t *normed_out,
+                                   uint16_t *ffn_residual, const uint16_t *attn,
+                                   const uint16_t *w_col_major, const uint16_t *norm_weight,
+                                   const uint16_t *x, int32_t rows, int32_t attention_width,
+                                   int32_t hidden, float eps) {
+  float *arow = (float *)malloc((size_t)attention_width * sizeof(float));
+  float *res = (float *)malloc((size_t)hidden * sizeof(float));
+  for (int32_t r = 0; r < rows; ++r) {
+    const uint16_t *a = attn + (int64_t)r * attention_width;
+    for (int32_t e = 0; e < attention_width; ++e) arow[e] = oracle_bf16_to_f32(a[e]);
+    for (int32_t c = 0; c < hidden; ++c) {
+      const uint16_t *w = w_col_major + (int64_t)c * attention_width;
+      double sum = 0.0;
+      for (int32_t e = 0; e < attention_width; ++e) sum += (double)arow[e] * oracle_bf16_to_f32(w[e]);
+      const uint16_t bits = oracle_f32_to_bf16((float)sum);
+      residual_out[(int64_t)r * hidden + c] = bits;
+      res[c] = oracle_bf16_to_f32(bits);
+    }
+    const float s = oracle_rms_scale(res, hidden, eps);
+    for (int32_t c = 0; c < hidden; ++c) {
+      const int64_t o = (int64_t)r * hidden + c;
+      const uint16_t n = oracle_f32_to_bf16(res[c] * s * oracle_bf16_to_f32(norm_weight[c]));
+      normed_out[o] = n;
+      ffn_residual[o] = oracle_f32_to_bf16(oracle_bf16_to_f32(x[o]) + oracle_bf16_to_f32(n));
+    }
+  }
+  free(arow);
+  free(res);
+}

@@ -22,6 +22,10 @@
  *   oracle_prefill_attention : torch float64 SDPA with explicit mask, the
  *                              reference q=0 running-mean known answer
  *                              (tests/test_flash_attention.cu:335-345)
+ *   oracle_attention_o_projection: float64 matmul (numpy), closed forms
+ *                              (one-hot attention row selects a weight
+ *                              element; a constant residual row normalises
+ *                              to the weight), residual identity
  *   oracle_rms_* / oracle_rope_*: reference known answers
  *                              (tests/test_flash_attention.cu:285-333,
  *                              tests/test_runtime_state.cu:110-140)
@@ -122,6 +126,11 @@ void oracle_prep_head(uint16_t *out, const uint16_t *in,
                       const uint16_t *weight /* NULL: scale-free */,
                       const float *cos_row, const float *sin_row,
                       int32_t head_dim, int32_t rotary_dim, float eps);
+void oracle_attention_o_projection(uint16_t *residual_out, uint16_t *normed_out,
+                                   uint16_t *ffn_residual, const uint16_t *attn,
+                                   const uint16_t *w_col_major, const uint16_t *norm_weight,
+                                   const uint16_t *x, int32_t rows, int32_t attention_width,
+                                   int32_t hidden, float eps);
 void oracle_fill_rope_tables(float *cos_table, float *sin_table,
                              int32_t max_seq_len, int32_t rotary_half,
                              float theta, int32_t exponent_dim);

@@ -58,6 +58,7 @@ def lib():
             "oracle_rms_scale": (F, [P, I, F]),
             "oracle_prep_head": (None, [P, P, P, P, P, I, I, F]),
             "oracle_fill_rope_tables": (None, [P, P, I, I, F, I]),
+            "oracle_attention_o_projection": (None, [P, P, P, P, P, P, P, I, I, I, F]),
             "oracle_f32_to_bf16_array": (None, [P, P, ctypes.c_int64]),
             "oracle_bf16_to_f32_array": (None, [P, P, ctypes.c_int64]),
         }
@@ -214,3 +215,19 @@ def fill_rope_tables(max_seq_len, rotary_half, theta, exponent_dim):
     lib().oracle_fill_rope_tables(_p(cos), _p(sin), max_seq_len, rotary_half, theta,
                                   exponent_dim)
     return cos, sin
+
+
+def attention_o_projection(attn, w_col_major, norm_weight, x, eps=1e-6):
+    """attn [rows][width], w_col_major [hidden][width], norm_weight [hidden],
+    x [rows][hidden] (bf16 bits) -> (residual_out, normed_out, ffn_residual)."""
+    attn = np.ascontiguousarray(attn, dtype=np.uint16)
+    w = np.ascontiguousarray(w_col_major, dtype=np.uint16)
+    g = np.ascontiguousarray(norm_weight, dtype=np.uint16)
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    rows, width = attn.shape
+    hidden = w.shape[0]
+    assert w.shape == (hidden, width) and g.shape == (hidden,) and x.shape == (rows, hidden)
+    outs = [np.zeros((rows, hidden), dtype=np.uint16) for _ in range(3)]
+    lib().oracle_attention_o_projection(*(_p(o) for o in outs), _p(attn), _p(w), _p(g), _p(x),
+                                        rows, width, hidden, eps)
+    return tuple(outs)

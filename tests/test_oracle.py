@@ -318,3 +318,61 @@ def test_prep_head_known_answers():
     assert abs(out[0] - (-hi)) <= 2 ** -7 and abs(out[half] - lo) <= 2 ** -7
     assert np.abs(out[1:half] - kf[1:half] * inv).max() <= 2 ** -7   # cos 1, sin 0: identity
     assert np.abs(out[128:] - kf[128:] * inv).max() <= 2 ** -7       # non-rotary tail
+
+
+# ---- attention output projection + post-attention norm -----------------------
+
+def _bf16_round(x):
+    return oracle.f32_to_bf16(np.asarray(x, dtype=np.float32))
+
+
+def test_o_projection_oracle_matches_float64_matmul():
+    rng = np.random.default_rng(7)
+    rows, width, hidden = 3, 512, 384
+    attn = randn_bf16(rng, (rows, width))
+    w = _bf16_round(rng.standard_normal((hidden, width)) * 0.05)
+    g = _bf16_round(1.0 + 0.1 * rng.standard_normal(hidden))
+    x = randn_bf16(rng, (rows, hidden))
+    res, normed, ffn = oracle.attention_o_projection(attn, w, g, x)
+    a64 = oracle.bf16_to_f32(attn).astype(np.float64)
+    w64 = oracle.bf16_to_f32(w).astype(np.float64)
+    want = _bf16_round(a64 @ w64.T)
+    diff = np.abs(res.astype(np.int32) - want.astype(np.int32))
+    assert diff.max() <= 1 and (diff == 0).mean() > 0.999
+    # RMSNorm of the bf16 residual row with the learned weight, in float64.
+    r64 = oracle.bf16_to_f32(res).astype(np.float64)
+    scale = 1.0 / np.sqrt((r64 ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    n64 = r64 * scale * oracle.bf16_to_f32(g).astype(np.float64)
+    got = oracle.bf16_to_f32(normed).astype(np.float64)
+    assert np.all(np.abs(got - n64) <= np.abs(n64) * 2.0 ** -8 + 1e-30)
+    # Residual: x + normed, one rounding.
+    s64 = oracle.bf16_to_f32(x).astype(np.float64) + got
+    assert np.array_equal(ffn, _bf16_round(s64))
+
+
+def test_o_projection_oracle_closed_forms():
+    rng = np.random.default_rng(8)
+    width, hidden = 256, 128
+    w = _bf16_round(rng.standard_normal((hidden, width)))
+    g = _bf16_round(0.5 + rng.random(hidden))
+    # A one-hot attention row selects one weight element per hidden column
+    # (catches a transposed weight: a column-major read would pick W[e0][c]).
+    e0 = 37
+    attn = np.zeros((1, width), dtype=np.uint16)
+    attn[0, e0] = 0x3F80  # 1.0
+    x = np.zeros((1, hidden), dtype=np.uint16)
+    res, normed, ffn = oracle.attention_o_projection(attn, w, g, x)
+    assert np.array_equal(res[0], w[:, e0])
+    assert np.array_equal(ffn, normed)  # x = 0
+    # A constant residual row (every W[c][e0] = 2) normalises to the weight.
+    w2 = w.copy()
+    w2[:, e0] = 0x4000  # 2.0
+    res, normed, _ = oracle.attention_o_projection(attn, w2, g, x)
+    assert np.all(res == 0x4000)
+    assert np.abs(normed.astype(np.int32) - g.astype(np.int32)).max() <= 1
+    # Negating the attention row negates the residual and the normed row.
+    attn_neg = attn ^ np.uint16(0x8000)
+    r1, n1, _ = oracle.attention_o_projection(attn, w, g, x)
+    r2, n2, _ = oracle.attention_o_projection(attn_neg, w, g, x)
+    assert np.array_equal(r1 ^ np.uint16(0x8000), r2)
+    assert np.array_equal(n1 ^ np.uint16(0x8000), n2)
