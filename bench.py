@@ -401,7 +401,7 @@ def bench_widened(torch, gk, dev):
         copies = max(2, -(-384 * 2**20 // wbytes))
         ws = [rnd((HIDDEN, width)) for _ in range(copies)]
         g = rnd((HIDDEN,))
-        for rows in (1, 8, 64):
+        for rows in (1, 4, 8, 16, 64):
             attn, x = rnd((rows, width)), rnd((rows, HIDDEN))
             outs = [torch.empty((rows, HIDDEN), dtype=torch.int16, device=dev) for _ in range(3)]
             turn = [0]

@@ -1,8 +1,9 @@
 """Attention output projection + post-attention RMSNorm + residual
 (gemma4_attention_o_projection_post_norm_bf16, reference
 src/gemma4_flash_attention_decode.cu:34-129) against the oracle:
-residual_out within one bf16 ulp (the oracle sums in float64, the GPU in
-fp32 pairs), normed_out and ffn_residual within the north-star tolerance,
+residual_out within one bf16 ulp plus the fp32 summation error (the oracle
+sums in float64, the GPU on MFMA in fp32), normed_out within the north-star
+tolerance (and one ulp of the tail applied to the GPU's own residual), ffn_residual exact on the GPU's normed row,
 and the closed forms the oracle tests pin (one-hot attention row selects a
 weight element, exactly)."""
 import numpy as np
@@ -45,16 +46,29 @@ def _run(dev, attn, w, g, x, stream=None):
     return [from_dev_bf16(t) for t in outs]
 
 
-@pytest.mark.parametrize("rows,width,seed", [(1, 4096, 1), (1, 8192, 2), (3, 4096, 3), (5, 8192, 4)])
+@pytest.mark.parametrize("rows,width,seed", [(1, 4096, 1), (1, 8192, 2), (3, 4096, 3), (5, 8192, 4),
+                                             (17, 4096, 5), (40, 8192, 6), (70, 4096, 7)])
 def test_o_projection_matches_oracle(dev, rows, width, seed):
     attn, w, g, x = _inputs(seed, rows, width)
     print(f"o_projection rows={rows} width={width} seed={seed}", flush=True)
     res, normed, ffn = _run(dev, attn, w, g, x)
     eres, enormed, effn = oracle.attention_o_projection(attn, w, g, x)
+    # Residual: one bf16 ulp of the float64 value, plus the fp32 summation
+    # error (relative to sum |a w|, which a sum that cancels to near zero
+    # makes large in ulps of the result).
     d = _ulp_diff(res, eres)
-    assert d.max() <= 1 and (d > 0).mean() < 0.02, (d.max(), (d > 0).mean())
+    assert (d > 0).mean() < 0.02, (d > 0).mean()
+    a64 = np.abs(oracle.bf16_to_f32(attn).astype(np.float64))
+    w64 = np.abs(oracle.bf16_to_f32(w).astype(np.float64))
+    mag = a64 @ w64.T
+    exp = oracle.bf16_to_f32(eres).astype(np.float64)
+    err = np.abs(oracle.bf16_to_f32(res) - exp)
+    ulp = np.maximum(np.abs(exp), 1e-30) * 2.0 ** -7
+    assert np.all(err <= ulp + 2.0 ** -16 * mag), float((err - ulp).max())
     assert_close(normed, enormed, "normed_out")
-    assert_close(ffn, effn, "ffn_residual")
+    # ffn_residual = x + normed cancels: a one-ulp step of normed (up to
+    # 2^-6 at magnitude 2..4) can be most of a small sum, so it is checked
+    # exactly against the GPU's own normed row below, not by tolerance.
     # The tail applied to the GPU's own residual row is the oracle's tail:
     # normed within one ulp, the residual add exact on the GPU's normed row.
     r32 = oracle.bf16_to_f32(res).astype(np.float64)
