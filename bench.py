@@ -321,6 +321,35 @@ def bench_batch64(torch, gk, dev, steps, warmup):
             "bytes_per_step": total}
 
 
+def bench_oproj(torch, gk, dev, rnd, rows_list=(1, 4, 8, 16, 64)):
+    """Attention output projection + post-attention norm + residual, per
+    launch pair. The weights rotate over copies that together exceed the
+    256 MiB MALL, so every launch streams its weights from HBM."""
+    oproj = {}
+    for width in (4096, 8192):
+        wbytes = HIDDEN * width * 2
+        copies = max(2, -(-384 * 2**20 // wbytes))
+        ws = [rnd((HIDDEN, width)) for _ in range(copies)]
+        g = rnd((HIDDEN,))
+        for rows in rows_list:
+            attn, x = rnd((rows, width)), rnd((rows, HIDDEN))
+            outs = [torch.empty((rows, HIDDEN), dtype=torch.int16, device=dev) for _ in range(3)]
+            turn = [0]
+
+            def fn(st):
+                w = ws[turn[0] % copies]
+                turn[0] += 1
+                gk.check(gk.attention_o_projection_post_norm_bf16(*outs, attn, w, g, x, rows, width,
+                                                                  stream=st), "o projection")
+            fn(torch.cuda.current_stream().cuda_stream)
+            us = time_each(torch, fn, 60) * 1e3
+            nbytes = wbytes + rows * (width + 4 * HIDDEN) * 2
+            oproj[f"width{width}_rows{rows}"] = {"us": round(us, 2),
+                                                 "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        del ws
+    return oproj
+
+
 def bench_widened(torch, gk, dev):
     """The rows around the hot path, each timed on its own: the decode-token
     prep + append (both geometries, batch 1 and 64), the prefill norm+RoPE
@@ -392,32 +421,7 @@ def bench_widened(torch, gk, dev):
         launch[name] = {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
     res["prefill_norm_rope_launchers"] = launch
 
-    # Attention output projection + post-attention norm + residual. The
-    # weights rotate over copies that together exceed the 256 MiB MALL, so
-    # every launch streams its weights from HBM.
-    oproj = {}
-    for width in (4096, 8192):
-        wbytes = HIDDEN * width * 2
-        copies = max(2, -(-384 * 2**20 // wbytes))
-        ws = [rnd((HIDDEN, width)) for _ in range(copies)]
-        g = rnd((HIDDEN,))
-        for rows in (1, 4, 8, 16, 64):
-            attn, x = rnd((rows, width)), rnd((rows, HIDDEN))
-            outs = [torch.empty((rows, HIDDEN), dtype=torch.int16, device=dev) for _ in range(3)]
-            turn = [0]
-
-            def fn(st):
-                w = ws[turn[0] % copies]
-                turn[0] += 1
-                gk.check(gk.attention_o_projection_post_norm_bf16(*outs, attn, w, g, x, rows, width,
-                                                                  stream=st), "o projection")
-            fn(torch.cuda.current_stream().cuda_stream)
-            us = time_each(torch, fn, 60) * 1e3
-            nbytes = wbytes + rows * (width + 4 * HIDDEN) * 2
-            oproj[f"width{width}_rows{rows}"] = {"us": round(us, 2),
-                                                 "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
-        del ws
-    res["attention_o_projection"] = oproj
+    res["attention_o_projection"] = bench_oproj(torch, gk, dev, rnd)
 
     # Runtime decode-step bookkeeping: host (validate, map, H2D copies) vs
     # device (one kernel), wall time per step with the stream drained.
@@ -507,7 +511,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-widened", action="store_true")
     ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill",
-                                       "widened"],
+                                       "widened", "oproj"],
                     default=None,
                     help="profiling helper: run one leg only")
     args = ap.parse_args()
@@ -537,6 +541,12 @@ def main():
         return
     if args.only == "widened":
         print(json.dumps(bench_widened(torch, gk, dev)))
+        return
+    if args.only == "oproj":
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(7)
+        rnd = lambda shape: torch.randn(shape, generator=gen, device=dev).bfloat16().view(torch.int16)
+        print(json.dumps(bench_oproj(torch, gk, dev, rnd, rows_list=(1, 64))))
         return
 
     layers, caches, meta, scratch = build_config2(torch, gk, dev)
