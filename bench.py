@@ -311,7 +311,7 @@ def bench_batch64(torch, gk, dev, steps, warmup):
     # Back-to-back eager launches (steady-state serving loop; the next step's
     # launch overlaps the current one). A graph replay per step measured
     # ~60 us slower per 1.4 ms step on this path.
-    ms = time_eager(torch, fn, max(steps, 10), max(warmup, 3))
+    ms = time_eager(torch, fn, max(steps, 20), max(warmup, 10))
     total = sum(layer_bytes(int(s)) for s in seq)
     gbs = total / (ms * 1e-3) / 1e9
     del ck, cv
@@ -319,6 +319,53 @@ def bench_batch64(torch, gk, dev, steps, warmup):
             "us_per_layer_step": ms * 1e3, "achieved_GBs": gbs,
             "frac_of_peak": gbs / HBM_PEAK_GBS, "split_size": split, "num_splits": n,
             "bytes_per_step": total}
+
+
+def bench_long(torch, gk, dev, steps, warmup, target_workgroups=0, counters=False, ctx=131072):
+    """one global layer, one sequence of 131072 keys (1 GiB
+    of K/V), 1% of the keys scaled x8; fused append + split kernel, then the
+    log-sum-exp combine (a second kernel, or in-kernel with counters)."""
+    page = GLOBAL_PAGE
+    max_pages = ctx // page
+    cfg = gk.make_config(1, max_pages, page, max_pages, 1, HEADS, DIM, 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(4)
+    ck = torch.empty((ctx, HEADS, DIM), dtype=torch.bfloat16, device=dev)
+    cv = torch.empty_like(ck)
+    for t in (ck, cv):
+        for r0 in range(0, ctx, 1 << 15):
+            n_rows = min(1 << 15, ctx - r0)
+            t[r0:r0 + n_rows] = torch.randn((n_rows, HEADS, DIM), generator=gen,
+                                            device=dev).bfloat16()
+    hot = torch.randperm(ctx, generator=gen, device=dev)[:ctx // 100]
+    ck[hot] *= 8
+    ck, cv = ck.view(torch.int16), cv.view(torch.int16)
+    pt = torch.arange(max_pages, dtype=torch.int32, device=dev)
+    seq_t = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    pos_t = torch.tensor([ctx - 1], dtype=torch.int32, device=dev)
+    q = torch.randn((1, QH, DIM), generator=gen, device=dev).bfloat16().view(torch.int16)
+    k = torch.randn((1, HEADS, DIM), generator=gen, device=dev).bfloat16().view(torch.int16)
+    v = torch.randn((1, HEADS, DIM), generator=gen, device=dev).bfloat16().view(torch.int16)
+    out = torch.zeros((1, QH, DIM), dtype=torch.int16, device=dev)
+    split, n = gk.decode_split_plan(cfg, 1, ctx, target_workgroups)
+    pm = torch.empty(QH * n, device=dev)
+    pl = torch.empty_like(pm)
+    pa = torch.empty(QH * n * DIM, device=dev)
+    cnt = torch.zeros(HEADS, dtype=torch.int32, device=dev) if counters else None
+
+    def fn(st):
+        gk.check(gk.flash_attention_append_decode_paged_bf16(
+            out, pm, pl, pa, q, ck, cv, pt, seq_t, pos_t, k, v, cfg, 0, 1 / 16, split, n, 1,
+            stream=st, split_counters=cnt), "long-context decode")
+
+    ms = time_eager(torch, fn, max(steps, 20), max(warmup, 10))
+    total = layer_bytes(ctx)
+    gbs = total / (ms * 1e-3) / 1e9
+    del ck, cv
+    return {"workload": "config4: 1 global layer, 1 seq, ctx 131072, 1% keys x8",
+            "us_per_layer_step": ms * 1e3, "achieved_GBs": gbs,
+            "frac_of_peak": gbs / HBM_PEAK_GBS, "split_size": split, "num_splits": n,
+            "in_kernel_combine": counters, "bytes_per_step": total}
 
 
 def bench_oproj(torch, gk, dev, rnd, rows_list=(1, 4, 8, 16, 64)):
@@ -508,6 +555,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch64", action="store_true")
+    ap.add_argument("--no-long", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-widened", action="store_true")
     ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill",
@@ -658,6 +706,10 @@ def main():
     if not args.no_batch64:
         b64 = bench_batch64(torch, gk, dev, max(3, args.steps // 5), 2)
         result["batch64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in b64.items()}
+    if not args.no_long:
+        lc = bench_long(torch, gk, dev, max(10, args.steps // 2), 3)
+        result["long_context"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                  for k, v in lc.items()}
     del caches, runner
     if not args.no_prefill:
         result["prefill_config5"] = bench_prefill(torch, gk, dev, max(5, args.steps // 2))

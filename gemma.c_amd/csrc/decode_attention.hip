@@ -822,11 +822,13 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
   } else {
     return hipErrorInvalidValue;
   }
-  // Default: eight split workgroups per CU for one sequence; a batch is
-  // sized by its longest sequence, so shorter ones leave workgroups idle:
-  // 32 per CU then (measured best on BASELINE config 3: 64 sequences, 512 to
+  // Default: one split workgroup per CU for one sequence (measured on 8193,
+  // 16384 and 131072 keys: fewer, longer splits stream as fast and make the
+  // combine cheaper; counts that are not a multiple of the CU count leave a
+  // tail). A batch is sized by its longest sequence, so shorter ones leave
+  // workgroups idle: 32 per CU then (measured best on 64 sequences of 512 to
   // 32768 keys).
-  if (target_workgroups <= 0) target_workgroups = batch_count > 1 ? 8192 : 2048;
+  if (target_workgroups <= 0) target_workgroups = batch_count > 1 ? 8192 : 256;
   const int64_t keys = (int64_t)std::max(max_live_keys, 1);
   const int64_t heads = (int64_t)batch_count * config.num_heads;
   int64_t splits_per_seq = (target_workgroups + heads - 1) / heads;

@@ -141,8 +141,8 @@ hipError_t gemma4_flash_attention_global_fwd_bf16_norm_rope(
     int seqlen_k, float softmax_scale, hipStream_t stream);
 
 // Split plan for the MI355X: the split size (a multiple of the kernel's key
-// wave chunk) that gives about `target_workgroups` split workgroups (0 = default,
-// eight per CU) for `batch_count` sequences of up to `max_live_keys` live keys,
+// wave chunk) that gives about `target_workgroups` split workgroups (0 = default:
+// one per CU for one sequence, 32 per CU for a batch) for `batch_count` sequences of up to `max_live_keys` live keys,
 // and the split count that covers `max_live_keys`. Replaces the fixed
 // GEMMA4_SLIDING_DECODE_SPLIT_SIZE (src/gemma4.h:24) and the active split
 // count of src/gemma4_decode_megakernel.cu:158-167.
