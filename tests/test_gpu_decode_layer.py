@@ -138,3 +138,105 @@ def test_decode_layer_steps_against_oracle_chain(dev):
     got_v = from_dev_bf16(d_cv).reshape(cv_h.shape)
     assert _ulp_diff(got_k, ck_h).max() <= 1
     assert _ulp_diff(got_v, cv_h).max() <= 1
+
+
+def test_prefill_then_decode_against_oracle(dev):
+    """The prompt-then-decode handoff of one sliding layer: the prefill
+    launcher (prep + causal windowed attention), the prefill cache write
+    (only the last `window` rows of each sequence reach the ring,
+    src/gemma4_prefill_megakernel.cu:189-207), then one decode step (prep +
+    append + attention) over the cache the prefill left. The cache equals the
+    oracle's write of the GPU's prepared rows bit for bit; attention outputs
+    are within the north-star tolerance of the oracle."""
+    import torch
+    rng = np.random.default_rng(22)
+    heads, dim, rotary, theta, window, page = 8, 256, 256, 10000.0, 64, 16
+    batch, seq = 2, 100
+    rows = batch * seq
+    max_pages = ring_pages(window, page)
+    cfg_t = cache_config(1, batch, page, max_pages, heads, dim, window)
+    cfg = gk.make_config(*cfg_t)
+    q = randn_bf16(rng, (rows, QH, dim))
+    k = randn_bf16(rng, (rows, heads, dim), scale=2.0)
+    v = randn_bf16(rng, (rows, heads, dim))
+    qw = oracle.f32_to_bf16(1.0 + 0.2 * rng.standard_normal(dim).astype(np.float32))
+    kw = oracle.f32_to_bf16(1.0 + 0.2 * rng.standard_normal(dim).astype(np.float32))
+    cos, sin = oracle.fill_rope_tables(256, rotary // 2, theta, dim)
+    pos = np.tile(np.arange(seq, dtype=np.int32), batch)
+    tb = np.repeat(np.arange(batch, dtype=np.int32), seq)
+    scale = 1.0 / 16.0
+    half = rotary // 2
+    d_cos, d_sin, d_qw, d_kw = to_dev(cos, dev), to_dev(sin, dev), to_dev(qw, dev), to_dev(kw, dev)
+
+    print("prefill launcher", flush=True)
+    out = empty_bf16((rows, QH, dim), dev)
+    qp, kp, vp = (empty_bf16(s, dev) for s in ((rows, QH, dim), (rows, heads, dim),
+                                                (rows, heads, dim)))
+    gk.check(gk.flash_attention_sliding_fwd_bf16_norm_rope(
+        out, qp, kp, vp, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), d_qw, d_kw, d_cos,
+        d_sin, to_dev(pos, dev), batch, seq, seq, window, scale), "sliding launcher")
+    pt = fill_page_table(cfg_t, [seq] * batch)
+    d_pt = to_dev(pt, dev)
+    cache_rows = batch * max_pages * page
+    ck0 = randn_bf16(rng, (cache_rows, heads, dim))  # stale ring contents
+    cv0 = randn_bf16(rng, (cache_rows, heads, dim))
+    d_ck, d_cv = to_dev(ck0, dev), to_dev(cv0, dev)
+    print("prefill cache write", flush=True)
+    gk.check(gk.kv_cache_write_prefill_bf16(d_ck, d_cv, cfg, d_pt, to_dev(tb, dev),
+                                            to_dev(pos, dev), batch, seq, 0, kp, vp),
+             "prefill write")
+    torch.cuda.synchronize()
+    got_out = from_dev_bf16(out)
+    kph = from_dev_bf16(kp).reshape(rows, heads, dim)
+    vph = from_dev_bf16(vp).reshape(rows, heads, dim)
+    qph = from_dev_bf16(qp).reshape(rows, QH, dim)
+    # Prefill attention vs the oracle on the GPU's prepared rows.
+    for b in range(batch):
+        sl = slice(b * seq, (b + 1) * seq)
+        exp = oracle.prefill_attention(qph[sl], kph[sl], vph[sl], seq, seq, QH, heads, dim,
+                                       window, scale)
+        assert_close(got_out.reshape(rows, QH, dim)[sl], exp, f"prefill attention batch {b}")
+    # Cache: the oracle's write of the last `window` rows of each sequence.
+    exp_ck, exp_cv = ck0.copy(), cv0.copy()
+    tail = np.concatenate([np.arange(b * seq + seq - window, (b + 1) * seq) for b in range(batch)])
+    oracle.kv_cache_write(exp_ck, exp_cv, cfg_t, pt, tb[tail], pos[tail], 0, kph[tail],
+                          vph[tail])
+    assert np.array_equal(from_dev_bf16(d_ck).reshape(exp_ck.shape), exp_ck)
+    assert np.array_equal(from_dev_bf16(d_cv).reshape(exp_cv.shape), exp_cv)
+
+    print("decode step after prefill", flush=True)
+    dpos = [seq] * batch
+    dseq = [seq + 1] * batch
+    pt = fill_page_table(cfg_t, dseq)
+    d_pt = to_dev(pt, dev)
+    q1 = randn_bf16(rng, (batch, QH, dim))
+    k1 = randn_bf16(rng, (batch, heads, dim), scale=2.0)
+    v1 = randn_bf16(rng, (batch, heads, dim))
+    d_qp1 = empty_bf16((batch, QH, dim), dev)
+    gk.check(gk.decode_prep_append_bf16(d_qp1, d_ck, d_cv, cfg, d_pt,
+                                        to_dev(np.asarray(dpos, np.int32), dev), 0,
+                                        to_dev(q1, dev), to_dev(k1, dev), to_dev(v1, dev), d_qw,
+                                        d_kw, d_cos, d_sin, batch), "decode prep")
+    split, n_splits = gk.decode_split_plan(cfg, batch, window)
+    pm = torch.empty(batch * QH * n_splits, device=dev)
+    pl = torch.empty_like(pm)
+    pa = torch.empty(batch * QH * n_splits * dim, device=dev)
+    d_att = empty_bf16((batch, QH, dim), dev)
+    gk.check(gk.flash_attention_decode_paged_bf16(d_att, pm, pl, pa, d_qp1, d_ck, d_cv, d_pt,
+                                                  to_dev(np.asarray(dseq, np.int32), dev), cfg,
+                                                  0, scale, split, n_splits, batch), "decode")
+    torch.cuda.synchronize()
+    exp_qp1 = np.zeros((batch, QH, dim), np.uint16)
+    kp1 = np.zeros((batch, heads, dim), np.uint16)
+    vp1 = np.zeros((batch, heads, dim), np.uint16)
+    p = seq
+    c_row, s_row = cos[p * half:(p + 1) * half], sin[p * half:(p + 1) * half]
+    for b in range(batch):
+        for h in range(QH):
+            exp_qp1[b, h] = oracle.prep_head(q1[b, h], qw, c_row, s_row, rotary)
+        for h in range(heads):
+            kp1[b, h] = oracle.prep_head(k1[b, h], kw, c_row, s_row, rotary)
+            vp1[b, h] = oracle.prep_head(v1[b, h], None, None, None, rotary)
+    oracle.kv_cache_write(exp_ck, exp_cv, cfg_t, pt, np.arange(batch), dpos, 0, kp1, vp1)
+    exp_att = oracle.decode_attention(exp_qp1, exp_ck, exp_cv, pt, dseq, cfg_t, 0, scale)
+    assert_close(from_dev_bf16(d_att).reshape(batch, QH, dim), exp_att, "decode after prefill")
