@@ -400,8 +400,10 @@ def bench_oproj(torch, gk, dev, rnd, rows_list=(1, 4, 8, 16, 64)):
 def bench_widened(torch, gk, dev):
     """The rows around the hot path, each timed on its own: the decode-token
     prep + append (both geometries, batch 1 and 64), the prefill norm+RoPE
-    launchers (prep + attention, 2048 rows), and the runtime's decode-step
-    bookkeeping on the host vs on the device. Synthetic N(0,1) inputs."""
+    launchers (prep + attention, 2048 rows), the attention output projection,
+    a decode layer from raw projections (two launches vs the fused one), and
+    the runtime's decode-step bookkeeping on the host vs on the device.
+    Synthetic N(0,1) inputs."""
     import time as _time
     import numpy as np
     res = {}
@@ -469,6 +471,47 @@ def bench_widened(torch, gk, dev):
     res["prefill_norm_rope_launchers"] = launch
 
     res["attention_o_projection"] = bench_oproj(torch, gk, dev, rnd)
+
+    # Decode layer from raw projections, config-2 shapes at batch 1: the
+    # token prep + append launch followed by the attention, against the
+    # fused call that prepares inside the attention launch.
+    fused = {}
+    for name, page, max_pages, window in (("sliding_ring1024", 1, WINDOW, WINDOW),
+                                          ("global_ctx8192", GLOBAL_PAGE,
+                                           (CONTEXT + GLOBAL_PAGE) // GLOBAL_PAGE, 0)):
+        cfg = gk.make_config(1, max_pages, page, max_pages, 1, HEADS, DIM, window)
+        rows = max_pages * page
+        ck, cv = rnd((rows, HEADS, DIM)), rnd((rows, HEADS, DIM))
+        pt = torch.arange(max_pages, dtype=torch.int32, device=dev)
+        seq_t = torch.tensor([CONTEXT + 1], dtype=torch.int32, device=dev)
+        pos_t = torch.tensor([CONTEXT], dtype=torch.int32, device=dev)
+        q, k, v = rnd((1, QH, DIM)), rnd((1, HEADS, DIM)), rnd((1, HEADS, DIM))
+        qp, out = torch.empty_like(q), torch.empty_like(q)
+        w = rnd((DIM,))
+        cos = torch.rand((CONTEXT + 1, DIM // 2), device=dev)
+        sin = torch.rand((CONTEXT + 1, DIM // 2), device=dev)
+        split, n = gk.decode_split_plan(cfg, 1, window if window else CONTEXT + 1)
+        pm = torch.empty(QH * n, device=dev)
+        pl = torch.empty_like(pm)
+        pa = torch.empty(QH * n * DIM, device=dev)
+
+        def two(st):
+            gk.check(gk.decode_prep_append_bf16(qp, ck, cv, cfg, pt, pos_t, 0, q, k, v, w, w, cos,
+                                                sin, 1, stream=st), "prep")
+            gk.check(gk.flash_attention_decode_paged_bf16(out, pm, pl, pa, qp, ck, cv, pt, seq_t,
+                                                          cfg, 0, 1 / 16, split, n, 1,
+                                                          stream=st), "decode")
+
+        def one(st):
+            gk.check(gk.flash_attention_prep_append_decode_paged_bf16(
+                out, pm, pl, pa, q, ck, cv, pt, seq_t, pos_t, k, v, w, w, cos, sin, cfg, 0,
+                1 / 16, split, n, 1, stream=st), "fused")
+        two(torch.cuda.current_stream().cuda_stream)
+        one(torch.cuda.current_stream().cuda_stream)
+        fused[name] = {"prep_then_attention_us": round(time_each(torch, two, 50) * 1e3, 2),
+                       "fused_us": round(time_each(torch, one, 50) * 1e3, 2)}
+        del ck, cv
+    res["decode_layer_from_raw_projections"] = fused
 
     # Runtime decode-step bookkeeping: host (validate, map, H2D copies) vs
     # device (one kernel), wall time per step with the stream drained.

@@ -24,6 +24,7 @@
 // stored split maxima are converted back to the reference's natural-log units.
 #include "gemma4_device.hpp"
 #include "decode_common.hpp"
+#include "prep_common.hpp"
 
 #include "gemma4_flash_attention.h"
 
@@ -49,6 +50,11 @@ struct DecodeParams {
   int32_t *counters;              // null: separate combine kernel
   const uint16_t *new_k;
   const uint16_t *new_v;
+  // Fused preparation (null q_norm_weight: q and the new K/V come prepared).
+  const uint16_t *q_norm_weight;
+  const uint16_t *k_norm_weight;
+  const float *cos;              // [position][rotary / 2]
+  const float *sin;
   Gemma4KvCacheConfig c;
   int32_t layer;
   float q_scale;  // softmax_scale * log2(e)
@@ -70,6 +76,9 @@ struct DecodeShape {
   static constexpr int S = __builtin_ctz(LPR / NP);       // duplicate-lane bits
   static constexpr int GB = __builtin_ctz(GW);            // head-select bits
   static constexpr int kRowElems = kHeads * kDim;
+  // Rotary dims of the geometry: all of a sliding head, a quarter of a
+  // global one (src/gemma4.h rotary settings).
+  static constexpr int kRot = kHeads == 1 ? kDim / 4 : kDim;
   static_assert(G % GW == 0, "heads per wave must divide the GQA group");
   static_assert(NP <= LPR, "one reduced score per lane at most");
   static_assert((NP & (NP - 1)) == 0 && (GW & (GW - 1)) == 0, "powers of two");
@@ -150,6 +159,55 @@ __device__ __forceinline__ void combine_row_group(const DecodeParams &p, int32_t
   }
 }
 
+// RMSNorm (learned weight, or scale-free with weight == null) and split-half
+// RoPE over the first kRot dims of one head held in this kernel's layout:
+// lane c of a row holds dims [8c, 8c + 8) of the D = 8 * LPR dims, so the sum
+// of squares is a reduction over the LPR lanes of the row and the rotary
+// partner of dim d (d + kRot/2 or d - kRot/2) sits kRot/16 lanes away.
+// Follows src/gemma4_flash_attention_decode.cu:233-283 and
+// src/gemma4_rope.cu:8-20; the result is rounded to bf16 as the reference
+// stores prepared rows.
+template <int LPR, int kRot>
+__device__ __forceinline__ uint4 prep_pack(uint4 raw, const uint16_t *weight,
+                                           const float *cos_row, const float *sin_row,
+                                           int cpack) {
+  float x[8];
+  unpack8(raw, x);
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+  ss += lane_xor<1>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<8>(ss);
+  ss += lane_xor<16>(ss);
+  if constexpr (LPR == 64) ss += lane_xor<32>(ss);
+  const float scale = 1.0f / sqrtf(ss / (float)(LPR * kPackElems) + kRmsEps);
+  float y[8];
+  if (weight == nullptr) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = x[i] * scale;
+  } else {
+    float w[8];
+    unpack8(load128(weight + cpack * kPackElems), w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = x[i] * scale * w[i];
+    constexpr int kHalf = kRot / 2;
+    float partner[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) partner[i] = lane_xor<kHalf / kPackElems>(y[i]);
+    const int d0 = cpack * kPackElems;
+    if (d0 < kRot) {
+      const int pair = d0 < kHalf ? d0 : d0 - kHalf;
+      const float sign = d0 < kHalf ? -1.0f : 1.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = fmaf(sign * partner[i], sin_row[pair + i], y[i] * cos_row[pair + i]);
+    }
+  }
+  return make_uint4(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                    pack_bf16x2(y[6], y[7]));
+}
+
 template <class Sh>
 __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeParams p) {
   constexpr int G = Sh::G, GW = Sh::GW, HG = Sh::HG, LPR = Sh::LPR, RPL = Sh::RPL;
@@ -184,19 +242,46 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
 
   // ---- fused append of the current token (one split per (b, head) owns it)
   int32_t new_pos = -1, new_row = -1;
+  const bool prep = p.q_norm_weight != nullptr;
   if (p.token_position != nullptr) {
     new_pos = wave_uniform(p.token_position[b]);
     new_row = wave_uniform(append_row(c, p.page_table, p.layer, b, new_pos));
     const bool in_live = new_pos >= first && new_pos < seq_len;
     const int32_t owner = in_live ? (new_pos - first) / p.split_size : 0;
-    if (split == owner && new_row >= 0 && threadIdx.x < LPR) {
-      const int64_t src = ((int64_t)b * c.num_heads + head) * D + threadIdx.x * kPackElems;
-      const int64_t dst = (int64_t)new_row * Sh::kRowElems + (int64_t)head * D +
-                          threadIdx.x * kPackElems;
-      store128(p.cache_k + dst, load128(p.new_k + src));
-      store128(p.cache_v + dst, load128(p.new_v + src));
+    const bool writes = split == owner && new_row >= 0;
+    if (prep) {
+      // Wave 0 prepares the token's K and V rows (both lane rows compute, the
+      // first stores) and writes them; the workgroup then reads the new key
+      // from the cache like any other, after the stores have completed.
+      if (writes && wave == 0) {
+        const int64_t src = ((int64_t)b * c.num_heads + head) * D + cpack * kPackElems;
+        const float *cos_row = p.cos + (int64_t)new_pos * (Sh::kRot / 2);
+        const float *sin_row = p.sin + (int64_t)new_pos * (Sh::kRot / 2);
+        const uint4 raw_k = load128(p.new_k + src);
+        const uint4 kp = prep_pack<LPR, Sh::kRot>(raw_k, p.k_norm_weight, cos_row, sin_row, cpack);
+        // The 1x512 geometry derives V from the raw K (no V projection).
+        const uint4 raw_v = p.new_v != nullptr ? load128(p.new_v + src) : raw_k;
+        const uint4 vp = prep_pack<LPR, Sh::kRot>(raw_v, nullptr, cos_row, sin_row, cpack);
+        if (r == 0) {
+          const int64_t dst = (int64_t)new_row * Sh::kRowElems + (int64_t)head * D +
+                              cpack * kPackElems;
+          store128(p.cache_k + dst, kp);
+          store128(p.cache_v + dst, vp);
+        }
+        wait_stores_complete();
+      }
+      if (writes) __syncthreads();
+      new_pos = -1;
+    } else {
+      if (writes && threadIdx.x < LPR) {
+        const int64_t src = ((int64_t)b * c.num_heads + head) * D + threadIdx.x * kPackElems;
+        const int64_t dst = (int64_t)new_row * Sh::kRowElems + (int64_t)head * D +
+                            threadIdx.x * kPackElems;
+        store128(p.cache_k + dst, load128(p.new_k + src));
+        store128(p.cache_v + dst, load128(p.new_v + src));
+      }
+      if (!in_live || new_row < 0) new_pos = -1;  // attention reads it from the cache path only if live
     }
-    if (!in_live || new_row < 0) new_pos = -1;  // attention reads it from the cache path only if live
   }
 
   if (key_count == 0 && direct) {
@@ -220,10 +305,18 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
   // Q stays packed bf16 (two dims per register): Q·K runs on v_dot2 with
   // exact products and fp32 sums; the softmax scale is applied to the sum.
   uint32_t qw[GW][4];
+  // With fused preparation q is normalised and rotated here, at the token's
+  // position (a sequence without a token this step uses q as given).
+  const bool prep_q = prep && wave_uniform(p.token_position[b]) >= 0;
+  const int32_t q_pos = prep_q ? wave_uniform(p.token_position[b]) : 0;
 #pragma unroll
   for (int g = 0; g < GW; ++g) {
     const int qh = head * G + hg * GW + g;
-    const uint4 qp = load128(p.q + ((int64_t)b * kQueryHeads + qh) * D + cpack * kPackElems);
+    uint4 qp = load128(p.q + ((int64_t)b * kQueryHeads + qh) * D + cpack * kPackElems);
+    if (prep_q) {
+      qp = prep_pack<LPR, Sh::kRot>(qp, p.q_norm_weight, p.cos + (int64_t)q_pos * (Sh::kRot / 2),
+                                    p.sin + (int64_t)q_pos * (Sh::kRot / 2), cpack);
+    }
     qw[g][0] = qp.x; qw[g][1] = qp.y; qw[g][2] = qp.z; qw[g][3] = qp.w;
   }
 
@@ -674,7 +767,9 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
                         const Gemma4KvCacheConfig &c,
                         int32_t layer, float softmax_scale, int32_t split_size,
                         int32_t num_splits, int32_t batch_count, bool combine,
-                        hipStream_t stream) {
+                        hipStream_t stream, const uint16_t *q_norm_weight = nullptr,
+                        const uint16_t *k_norm_weight = nullptr, const float *cos = nullptr,
+                        const float *sin = nullptr) {
   if (batch_count == 0) return hipSuccess;
   if (batch_count < 0 || batch_count > c.batch_size || batch_count > 65535 || num_splits > 65535 ||
       !valid_decode_config(c, layer) || !(softmax_scale > 0.0f) ||
@@ -700,6 +795,10 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
   p.counters = num_splits > 1 ? counters : nullptr;
   p.new_k = new_k;
   p.new_v = new_v;
+  p.q_norm_weight = q_norm_weight;
+  p.k_norm_weight = k_norm_weight;
+  p.cos = cos;
+  p.sin = sin;
   p.c = c;
   p.layer = layer;
   p.q_scale = softmax_scale * kLog2e;
@@ -757,6 +856,33 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
       reinterpret_cast<const uint16_t *>(d_v), d_split_counters, config, layer,
       softmax_scale,
       split_size, num_splits, batch_count, /*combine=*/true, stream);
+}
+
+hipError_t gemma4_flash_attention_prep_append_decode_paged_bf16(
+    gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
+    float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+    const int32_t *d_seq_lengths, const int32_t *d_token_position,
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, const gemma4_bf16 *d_q_norm_weight,
+    const gemma4_bf16 *d_k_norm_weight, const float *d_cos, const float *d_sin,
+    int32_t *d_split_counters, Gemma4KvCacheConfig config, int32_t layer,
+    float softmax_scale, int32_t split_size, int32_t num_splits, int32_t batch_count,
+    hipStream_t stream) {
+  const bool global = config.num_heads == 1;
+  if (d_token_position == nullptr || d_k == nullptr || (d_v == nullptr && !global) ||
+      d_q_norm_weight == nullptr || d_k_norm_weight == nullptr || d_cos == nullptr ||
+      d_sin == nullptr) {
+    return hipErrorInvalidValue;
+  }
+  return decode_entry(
+      reinterpret_cast<uint16_t *>(d_out), d_partial_m, d_partial_l, d_partial_acc,
+      reinterpret_cast<const uint16_t *>(d_q), reinterpret_cast<uint16_t *>(d_cache_k),
+      reinterpret_cast<uint16_t *>(d_cache_v), d_page_table, d_seq_lengths,
+      d_token_position, reinterpret_cast<const uint16_t *>(d_k),
+      global ? nullptr : reinterpret_cast<const uint16_t *>(d_v), d_split_counters, config,
+      layer, softmax_scale, split_size, num_splits, batch_count, /*combine=*/true, stream,
+      reinterpret_cast<const uint16_t *>(d_q_norm_weight),
+      reinterpret_cast<const uint16_t *>(d_k_norm_weight), d_cos, d_sin);
 }
 
 hipError_t gemma4_flash_attention_decode_split_paged_bf16(

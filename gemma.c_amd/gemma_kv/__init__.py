@@ -85,6 +85,8 @@ SIGNATURES = {
         _I32, [_P] * 12 + [_I32, _I32, _I32, _I32, _F32, _P]),
     "gemma4_flash_attention_global_fwd_bf16_norm_rope": (
         _I32, [_P] * 11 + [_I32, _I32, _I32, _F32, _P]),
+    "gemma4_flash_attention_prep_append_decode_paged_bf16": (
+        _I32, [_P] * 17 + [_CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_attention_o_projection_post_norm_bf16": (_I32, [_P] * 7 + [_I32, _I32, _P]),
     "gemma4_runtime_create": (_I32, [ctypes.POINTER(_P), _I32, _I32, _I32, _P]),
     "gemma4_runtime_destroy": (None, [_P]),
@@ -391,6 +393,20 @@ def flash_attention_global_fwd_bf16_norm_rope(out, q_prepared, k_prepared, v_pre
         ptr(out), ptr(q_prepared), ptr(k_prepared), ptr(v_prepared), ptr(q), ptr(k),
         ptr(q_norm_weight), ptr(k_norm_weight), ptr(cos), ptr(sin), ptr(token_position),
         batch_size, seqlen_q, seqlen_k, softmax_scale, stream_handle(stream))
+
+
+def flash_attention_prep_append_decode_paged_bf16(out, partial_m, partial_l, partial_acc, q,
+                                                  cache_k, cache_v, page_table, seq_lengths,
+                                                  token_position, k, v, q_norm_weight,
+                                                  k_norm_weight, cos, sin, config, layer,
+                                                  softmax_scale, split_size, num_splits,
+                                                  batch_count, stream=None,
+                                                  split_counters=None) -> int:
+    return lib().gemma4_flash_attention_prep_append_decode_paged_bf16(
+        ptr(out), ptr(partial_m), ptr(partial_l), ptr(partial_acc), ptr(q), ptr(cache_k),
+        ptr(cache_v), ptr(page_table), ptr(seq_lengths), ptr(token_position), ptr(k), ptr(v),
+        ptr(q_norm_weight), ptr(k_norm_weight), ptr(cos), ptr(sin), ptr(split_counters), config,
+        layer, softmax_scale, split_size, num_splits, batch_count, stream_handle(stream))
 
 
 def attention_o_projection_post_norm_bf16(residual_out, normed_out, ffn_residual, attention_out,

@@ -67,6 +67,30 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
     int32_t split_size, int32_t num_splits, int32_t batch_count,
     hipStream_t stream);
 
+// Fused decode layer attention for raw projections: prepares q (learned
+// RMSNorm + RoPE at d_token_position[b]) inside every split workgroup, has the
+// split that owns the new key prepare its K (RMSNorm + RoPE) and V
+// (scale-free RMSNorm; derived from the raw K when config.num_heads == 1,
+// d_v may then be null) and write them into the cache, then attends exactly
+// as gemma4_flash_attention_append_decode_paged_bf16. One launch replaces
+// gemma4_decode_prep_append_bf16 followed by the append+decode call: the
+// reference's fused layer phases phase_decode_q_paged_kv_norm_rope +
+// split + reduce (src/gemma4_flash_attention_decode.cu:216-375, 691-977).
+// d_q / d_k / d_v are the raw [batch_count][heads][head_dim] rows; cos/sin
+// are [position][rotary/2] (rotary = head_dim for 8x256, head_dim/4 for
+// 1x512). A sequence with d_token_position[b] < 0 appends nothing and uses
+// its q as given. The prepared q is not written out.
+hipError_t gemma4_flash_attention_prep_append_decode_paged_bf16(
+    gemma4_bf16 *d_out, float *d_partial_m, float *d_partial_l,
+    float *d_partial_acc, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+    const int32_t *d_seq_lengths, const int32_t *d_token_position,
+    const gemma4_bf16 *d_k, const gemma4_bf16 *d_v, const gemma4_bf16 *d_q_norm_weight,
+    const gemma4_bf16 *d_k_norm_weight, const float *d_cos, const float *d_sin,
+    int32_t *d_split_counters, Gemma4KvCacheConfig config, int32_t layer,
+    float softmax_scale, int32_t split_size, int32_t num_splits, int32_t batch_count,
+    hipStream_t stream);
+
 // The two phases of gemma4_flash_attention_decode_paged_bf16 as separate
 // launches, for callers that schedule them apart (or time them): the split
 // phase (phase_decode_paged_grouped_split,
