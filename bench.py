@@ -159,6 +159,50 @@ def time_graph(torch, fn, reps, warmup):
     return start.elapsed_time(stop) / reps, g
 
 
+def warm_clock(torch, fn, seconds=0.3):
+    """Run fn(stream) back to back for `seconds`: a fresh process runs its
+    first ~0.1 s of sustained work up to 15% slower (clock ramp)."""
+    import time as _time
+    st = torch.cuda.current_stream().cuda_stream
+    t_end = _time.perf_counter() + seconds
+    while _time.perf_counter() < t_end:
+        for _ in range(10):
+            fn(st)
+        torch.cuda.synchronize()
+
+
+def time_graph_calls(torch, fn, calls, reps=5, warmup=2):
+    """Capture `calls` back-to-back invocations fn(stream, i) as one HIP graph
+    and replay it; returns ms per invocation. For kernels of a few to tens of
+    microseconds, whose eager launches would be paced by the host."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn(s.cuda_stream, 0)  # warm the code objects outside capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(calls):
+            fn(st, i)
+    import time as _time
+    t_end = _time.perf_counter() + 0.2  # past the clock ramp of a fresh process
+    n = 0
+    while n < warmup or _time.perf_counter() < t_end:
+        g.replay()
+        torch.cuda.synchronize()
+        n += 1
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        g.replay()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / (reps * calls)
+
+
 class StepRunner:
     """The whole config-2 step as one persistent launch."""
 
@@ -210,16 +254,18 @@ def bench_prefill(torch, gk, dev, reps):
         out = torch.zeros((1, lq, QH, DIM), dtype=torch.int16, device=dev)
         pr = torch.tensor([prior], dtype=torch.int32, device=dev)
 
-        def fn(st):
-            gk.check(gk.flash_attention_prefill_chunk_paged_bf16(
-                out, q, k, v, ck, cv, pt, pr, cfg, 0, 1, lq, 1 / 16, stream=st), "prefill")
+        raw = gk.lib().gemma4_flash_attention_prefill_chunk_paged_bf16
+        args = [gk.ptr(t) for t in (out, q, k, v, ck, cv, pt, pr)] + [cfg, 0, 1, lq, 1 / 16]
 
-        # Back-to-back eager launches: each chunk is long enough that the
-        # launch cost hides behind the previous one (a graph replay per
-        # launch would add its own overhead to every chunk).
-        # ~50 warm-up launches: the first tens of milliseconds of a fresh
-        # process run several percent slower (clock ramp).
-        ms = time_eager(torch, fn, max(reps, 50), 50)
+        def fn(st):
+            code = raw(*args, st)
+            if code:
+                raise gk.HipError(code, "prefill")
+
+        # Back-to-back eager launches through the raw C-ABI call, after a
+        # time-based warm-up (50 short chunks are shorter than the clock ramp).
+        warm_clock(torch, fn)
+        ms = time_eager(torch, fn, max(reps, 50), 10)
         keys = np.arange(lq) + prior + 1
         if window:
             keys = np.minimum(keys, window)
@@ -311,6 +357,7 @@ def bench_batch64(torch, gk, dev, steps, warmup):
     # Back-to-back eager launches (steady-state serving loop; the next step's
     # launch overlaps the current one). A graph replay per step measured
     # ~60 us slower per 1.4 ms step on this path.
+    warm_clock(torch, fn)
     ms = time_eager(torch, fn, max(steps, 20), max(warmup, 10))
     total = sum(layer_bytes(int(s)) for s in seq)
     gbs = total / (ms * 1e-3) / 1e9
@@ -358,6 +405,7 @@ def bench_long(torch, gk, dev, steps, warmup, target_workgroups=0, counters=Fals
             out, pm, pl, pa, q, ck, cv, pt, seq_t, pos_t, k, v, cfg, 0, 1 / 16, split, n, 1,
             stream=st, split_counters=cnt), "long-context decode")
 
+    warm_clock(torch, fn)
     ms = time_eager(torch, fn, max(steps, 20), max(warmup, 10))
     total = layer_bytes(ctx)
     gbs = total / (ms * 1e-3) / 1e9
@@ -369,9 +417,10 @@ def bench_long(torch, gk, dev, steps, warmup, target_workgroups=0, counters=Fals
 
 
 def bench_oproj(torch, gk, dev, rnd, rows_list=(1, 4, 8, 16, 64)):
-    """Attention output projection + post-attention norm + residual, per
-    launch pair. The weights rotate over copies that together exceed the
-    256 MiB MALL, so every launch streams its weights from HBM."""
+    """Attention output projection + post-attention norm + residual, per call
+    (projection + tail launches) from a graph of back-to-back calls. The
+    weights rotate over copies that together exceed the 256 MiB MALL, so
+    every call streams its weights from HBM."""
     oproj = {}
     for width in (4096, 8192):
         wbytes = HIDDEN * width * 2
@@ -381,15 +430,11 @@ def bench_oproj(torch, gk, dev, rnd, rows_list=(1, 4, 8, 16, 64)):
         for rows in rows_list:
             attn, x = rnd((rows, width)), rnd((rows, HIDDEN))
             outs = [torch.empty((rows, HIDDEN), dtype=torch.int16, device=dev) for _ in range(3)]
-            turn = [0]
 
-            def fn(st):
-                w = ws[turn[0] % copies]
-                turn[0] += 1
-                gk.check(gk.attention_o_projection_post_norm_bf16(*outs, attn, w, g, x, rows, width,
-                                                                  stream=st), "o projection")
-            fn(torch.cuda.current_stream().cuda_stream)
-            us = time_each(torch, fn, 60) * 1e3
+            def fn(st, i):
+                gk.check(gk.attention_o_projection_post_norm_bf16(
+                    *outs, attn, ws[i % copies], g, x, rows, width, stream=st), "o projection")
+            us = time_graph_calls(torch, fn, 4 * copies) * 1e3
             nbytes = wbytes + rows * (width + 4 * HIDDEN) * 2
             oproj[f"width{width}_rows{rows}"] = {"us": round(us, 2),
                                                  "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -431,11 +476,11 @@ def bench_widened(torch, gk, dev):
             cos = torch.rand((1024, rot // 2), device=dev)
             sin = torch.rand((1024, rot // 2), device=dev)
 
-            def fn(st):
+            def fn(st, i):
                 gk.check(gk.decode_prep_append_bf16(qp, ck, cv, cfg, pt, pos, 0, q, k,
                                                     v if heads > 1 else None, w, w, cos, sin,
                                                     batch, stream=st), "decode prep")
-            us = time_each(torch, fn, 50) * 1e3
+            us = time_graph_calls(torch, fn, 20) * 1e3
             nbytes = batch * (2 * QH * dim * 2 + 4 * heads * dim * 2)  # q in/out, k,v in, cache rows out
             prep[f"{name}_batch{batch}"] = {"us": round(us, 2),
                                             "GBs": round(nbytes / (us * 1e-6) / 1e9, 1)}
@@ -465,7 +510,7 @@ def bench_widened(torch, gk, dev):
                     out, qp, kp, vp, q, k, w, w, cos, sin, pos, 1, lq, lq, scale, stream=st),
                     "global launcher")
             keys = np.arange(lq) + 1
-        ms = time_eager(torch, fn, 20, 5)
+        ms = time_graph_calls(torch, lambda st, i: fn(st), 10)
         flops = 4 * dim * QH * int(keys.sum())
         launch[name] = {"us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
     res["prefill_norm_rope_launchers"] = launch
@@ -495,21 +540,21 @@ def bench_widened(torch, gk, dev):
         pl = torch.empty_like(pm)
         pa = torch.empty(QH * n * DIM, device=dev)
 
-        def two(st):
+        def two(st, i=0):
             gk.check(gk.decode_prep_append_bf16(qp, ck, cv, cfg, pt, pos_t, 0, q, k, v, w, w, cos,
                                                 sin, 1, stream=st), "prep")
             gk.check(gk.flash_attention_decode_paged_bf16(out, pm, pl, pa, qp, ck, cv, pt, seq_t,
                                                           cfg, 0, 1 / 16, split, n, 1,
                                                           stream=st), "decode")
 
-        def one(st):
+        def one(st, i=0):
             gk.check(gk.flash_attention_prep_append_decode_paged_bf16(
                 out, pm, pl, pa, q, ck, cv, pt, seq_t, pos_t, k, v, w, w, cos, sin, cfg, 0,
                 1 / 16, split, n, 1, stream=st), "fused")
         two(torch.cuda.current_stream().cuda_stream)
         one(torch.cuda.current_stream().cuda_stream)
-        fused[name] = {"prep_then_attention_us": round(time_each(torch, two, 50) * 1e3, 2),
-                       "fused_us": round(time_each(torch, one, 50) * 1e3, 2)}
+        fused[name] = {"prep_then_attention_us": round(time_graph_calls(torch, two, 20) * 1e3, 2),
+                       "fused_us": round(time_graph_calls(torch, one, 20) * 1e3, 2)}
         del ck, cv
     res["decode_layer_from_raw_projections"] = fused
 
