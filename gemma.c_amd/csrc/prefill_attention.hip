@@ -500,6 +500,15 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
 #pragma unroll
       for (int d = 0; d < DB; ++d) acc[d] = mfma32(vf[d], pb, acc[d]);
     }
+    // The block's 32 transposing V reads run two MFMAs ahead of its 16 P.V
+    // MFMAs (the compiler's own order waits on each MFMA's reads right before
+    // it; measured against 2 to 6 MFMAs of lead: 5-6% faster at this one).
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // 4 DS reads
+    static_for<0, 14>([](auto) __attribute__((always_inline)) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 DS reads
+    });
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
   };
 
   // ---- pipeline: copy tile i+1 and look up tile i+2 while computing i -----
