@@ -326,6 +326,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
 
   if (wave == kControlWave) {
     // ------------------------------------------------------------ control
+    // The control wave carries the per-layer chain (flags, inputs, combine):
+    // it issues ahead of the compute wave sharing its SIMD (measured 1.3%
+    // off the step; raising the compute waves over the prefetch wave too
+    // changed nothing).
+    __builtin_amdgcn_s_setprio(3);
     bool abort = false;
     // A split longer than the row tables hold would drop keys: report it.
     for (int kind = 0; kind < 2; ++kind) {
