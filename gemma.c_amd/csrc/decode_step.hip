@@ -48,8 +48,10 @@
 //   * layer completion: each workgroup stores its output chunks
 //     device-coherently, waits for them, then sets its XCD-local flag; the
 //     XCD's ticket-0 workgroup collects the 32 local flags and sets the XCD's
-//     device-coherent flag; every workgroup waits for all 8 XCD flags
-//     before reading the next layer's q. Flags hold the launch epoch
+//     device-coherent flag. Ticket 0 polls all 8 XCD flags and then raises
+//     the XCD's go flag in its L2; the other 31 workgroups poll that (an L2
+//     round trip, so they start the next layer together) before reading the
+//     next layer's q. Flags hold the launch epoch
 //     (1 + the value the previous launch left in the workspace header), so
 //     they never need clearing.
 // The XCD mapping needs exactly 32 workgroups per XCD; workspace
@@ -127,6 +129,7 @@ struct StepParams {
   uint32_t *tickets;      // [xcd * kTicketStride]
   int32_t *local_flags;   // [layer][xcd][slot]
   int32_t *global_flags;  // [layer][kGlobalFlagStride]
+  int32_t *go_flags;      // [layer][xcd][16]: XCD-local copy of "layer complete"
   float *records;
   int32_t *probe;         // non-null: only report each workgroup's XCD id
   int32_t batch;
@@ -342,12 +345,30 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         coherent_store_i32(p.header + kHeaderError, 2);
     }
     // Layer `layer_i` is complete once all 8 XCD flags read `epoch`.
-    auto wait_layer = [&](int32_t layer_i) {
+    auto wait_layer_device = [&](int32_t layer_i) {
       const int32_t *row = p.global_flags + layer_i * kGlobalFlagStride;
       const uint64_t t0 = now_ticks();
       while (!abort) {
         const bool ok = lane >= kXcds || coherent_load_i32(row + lane) == epoch;
         if (__ballot(!ok) == 0) break;
+        if (now_ticks() - t0 > kWaitTicks) abort = true;
+      }
+    };
+    // Ticket 0 of each XCD polls the 8 device flags and raises the XCD's
+    // go flag in its L2; the other 31 workgroups poll that (an L2 round
+    // trip, so they start together).
+    const BufferRsrc go_buf = buffer_of(p.go_flags, (int64_t)kNumModelLayers * kXcds * 16 * 4);
+    auto wait_layer = [&](int32_t layer_i) {
+      const int32_t off = ((layer_i * kXcds + xcd) * 16) * 4;
+      if (ticket == 0) {
+        wait_layer_device(layer_i);
+        if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)epoch, go_buf, off, 0, 0);
+        return;
+      }
+      const uint64_t t0 = now_ticks();
+      while (!abort) {
+        const int32_t v = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(go_buf, off, 0, kLocalLoadAux);
+        if (v == epoch) break;
         if (now_ticks() - t0 > kWaitTicks) abort = true;
       }
     };
@@ -815,10 +836,10 @@ __global__ void decode_step_workspace_init_kernel(int32_t *ints, int64_t n_ints,
 }
 
 // Workspace: header | XCD ticket counters | local flags | global flags |
-// probe slots | split records (sentinel-filled).
+// probe slots | go flags | split records (sentinel-filled).
 struct WorkspaceLayout {
   int32_t units, splits;
-  int64_t tickets, local_flags, global_flags, probe, int_count, record_floats, bytes;
+  int64_t tickets, local_flags, global_flags, probe, go_flags, int_count, record_floats, bytes;
 };
 WorkspaceLayout workspace_layout(int32_t batch_count) {
   WorkspaceLayout w{};
@@ -828,7 +849,8 @@ WorkspaceLayout workspace_layout(int32_t batch_count) {
   w.local_flags = w.tickets + kXcds * kTicketStride;
   w.global_flags = w.local_flags + (int64_t)kNumModelLayers * kXcds * kXcdSlots;
   w.probe = w.global_flags + (int64_t)kNumModelLayers * kGlobalFlagStride;
-  w.int_count = w.probe + kStepWorkgroups;
+  w.go_flags = w.probe + kStepWorkgroups;
+  w.int_count = w.go_flags + (int64_t)kNumModelLayers * kXcds * 16;
   w.record_floats = (int64_t)w.units * w.splits * kRecordFloats;
   w.bytes = (w.int_count + w.record_floats) * 4;
   return w;
@@ -844,6 +866,7 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
   p.tickets = reinterpret_cast<uint32_t *>(ints + w.tickets);
   p.local_flags = ints + w.local_flags;
   p.global_flags = ints + w.global_flags;
+  p.go_flags = ints + w.go_flags;
   p.records = reinterpret_cast<float *>(ints + w.int_count);
   p.batch = batch_count;
   p.units = w.units;
