@@ -874,8 +874,20 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
   return p;
 }
 
-hipError_t launch_step(StepParams &p, hipStream_t stream) {
+// The placement probe at workspace initialisation is a cooperative launch:
+// it checks that all 256 workgroups are resident together, one per CU and 32
+// per XCD (the 157 KB of LDS a workgroup takes leaves room for no second
+// one on a CU). The steps themselves are ordinary launches: a cooperative
+// launch costs ~18 us more per step to dispatch (405 vs 387 us per config-2
+// step), and on a GPU the step has to itself every workgroup is resident
+// anyway. Should another kernel hold CUs during a step, the bounded waits
+// expire and the status reports it; nothing hangs.
+hipError_t launch_step(StepParams &p, hipStream_t stream, bool cooperative) {
   void *args[] = {&p};
+  if (!cooperative) {
+    return hipLaunchKernel(reinterpret_cast<const void *>(decode_step_kernel),
+                           dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds, stream);
+  }
   return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(decode_step_kernel),
                                     dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds,
                                     stream);
@@ -918,7 +930,7 @@ extern "C" hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t 
     // 32 of its workgroups (one per CU) for the XCD-local exchange.
     StepParams p = base_params(workspace, w, batch_count);
     p.probe = ints + w.probe;
-    e = launch_step(p, stream);
+    e = launch_step(p, stream, /*cooperative=*/true);
     if (e != hipSuccess) return e;
     int32_t ids[kStepWorkgroups];
     e = hipMemcpyAsync(ids, p.probe, sizeof(ids), hipMemcpyDeviceToHost, stream);
@@ -1000,5 +1012,5 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
   p.first_layer = first_layer;
   p.layer_count = layer_count;
   p.q_scale = scale * kLog2e;
-  return launch_step(p, stream);
+  return launch_step(p, stream, /*cooperative=*/false);
 }

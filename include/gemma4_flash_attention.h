@@ -194,7 +194,9 @@ hipError_t gemma4_decode_prep_append_bf16(
     const float *sin, int32_t batch_count, hipStream_t stream);
 
 // ---- persistent decode step over consecutive layers --------------------
-// One cooperative launch that runs, for model layers first_layer ..
+// One persistent launch (256 workgroups, one per CU, all resident together:
+// the GPU must not run other kernels during the step) that runs, for model
+// layers first_layer ..
 // first_layer + layer_count - 1 in order, the fused K/V append of the current
 // token and the split-K decode attention with its combine, for `batch_count`
 // sequences. Replaces the per-layer attention launches of the reference
@@ -213,8 +215,8 @@ hipError_t gemma4_decode_prep_append_bf16(
 // gemma4_decode_step_workspace_init, then reuse it for every step (stream
 // order). Calls sharing a workspace must not overlap. After a call,
 // gemma4_decode_step_status reports 0, or a nonzero code if a bounded wait
-// expired (1; the workspace must then be initialised again) or a split
-// exceeded the 512-key table (2).
+// expired (1, e.g. another kernel held CUs; the workspace must then be
+// initialised again) or a split exceeded the 512-key table (2).
 size_t gemma4_decode_step_workspace_bytes(int32_t batch_count);
 hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t workspace_bytes,
                                              int32_t batch_count, hipStream_t stream);
