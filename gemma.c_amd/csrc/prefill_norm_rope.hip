@@ -154,7 +154,10 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
   const int g = lane >> 4;      // lane group: keys / dims 4g..4g+3 of the accumulator
   const int b = blockIdx.y;
   const int L = p.seq_len;
-  const int r0 = blockIdx.x * kD512Rows;
+  // Causal work grows with the row: the last rows are dispatched first, so
+  // the workgroups of the first rows fill the CUs that free up early
+  // (longest-first order; one workgroup per CU at a time).
+  const int r0 = (gridDim.x - 1 - blockIdx.x) * kD512Rows;
   const int row = r0 + wave;
   const bool row_ok = row < L;
   const int last_key = min(r0 + kD512Rows, L) - 1;  // last key any row of the workgroup sees
