@@ -319,6 +319,56 @@ def read_traffic(kernel_tag: str):
     return float(m.group(1)) if m else None
 
 
+def bench_config1(torch, gk, dev, reps=3):
+    """BASELINE config 1 on the GPU: one sliding layer, 1024-slot page-1 ring,
+    2048 sequential steps from an empty cache, each one fused append + decode
+    launch (the ring slot of position t is mapped from the start: the slots a
+    step cannot see yet are never read, so the work equals the reference
+    loop's). Step t's seq_len/position come from per-step device arrays. The
+    2048 launches are captured once as a graph and replayed (every replay
+    redoes the same 2048 appends and attentions)."""
+    steps = 2048
+    cfg = gk.make_config(1, WINDOW, 1, WINDOW, 1, HEADS, DIM, WINDOW)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=gen, device=dev).bfloat16().view(torch.int16)
+
+    q, k, v = rnd((steps, QH, DIM)), rnd((steps, HEADS, DIM)), rnd((steps, HEADS, DIM))
+    ck = torch.zeros((WINDOW, HEADS, DIM), dtype=torch.int16, device=dev)
+    cv = torch.zeros_like(ck)
+    pt = torch.arange(WINDOW, dtype=torch.int32, device=dev)
+    seq = torch.arange(1, steps + 1, dtype=torch.int32, device=dev)
+    pos = torch.arange(steps, dtype=torch.int32, device=dev)
+    out = torch.zeros((steps, QH, DIM), dtype=torch.int16, device=dev)
+    split, n = gk.decode_split_plan(cfg, 1, WINDOW)
+    pm = torch.empty(QH * n, device=dev)
+    pl = torch.empty_like(pm)
+    pa = torch.empty(QH * n * DIM, device=dev)
+    qrow, kvrow = QH * DIM * 2, HEADS * DIM * 2
+    lib = gk.lib()
+    base = [gk.ptr(t) for t in (out, pm, pl, pa, q, ck, cv, pt, seq, pos, k, v)]
+
+    def fn(st, i=0):
+        for t in range(steps):
+            code = lib.gemma4_flash_attention_append_decode_paged_bf16(
+                base[0] + t * qrow, base[1], base[2], base[3], base[4] + t * qrow, base[5],
+                base[6], base[7], base[8] + 4 * t, base[9] + 4 * t, base[10] + t * kvrow,
+                base[11] + t * kvrow, 0, cfg, 0, 1.0 / 16, split, n, 1, st)
+            if code:
+                raise gk.HipError(code, f"config1 step {t}")
+
+    ms = time_graph_calls(torch, fn, 1, reps=reps, warmup=1)
+    total = sum(layer_bytes(min(t + 1, WINDOW)) for t in range(steps))
+    return {"workload": "config1: 1 sliding layer, ring 1024 page 1, 2048 sequential "
+                        "append+attend steps from an empty cache",
+            "us_per_layer_step": round(ms * 1e3 / steps, 3), "ms_2048_steps": round(ms, 3),
+            "achieved_GBs": round(total / (ms * 1e-3) / 1e9, 1), "bytes_2048_steps": total,
+            "split_size": split, "num_splits": n,
+            "timing": "hipGraph of the 2048 fused launches, replayed"}
+
+
 def bench_batch64(torch, gk, dev, steps, warmup):
     """one global layer, 64 sequences, contexts U[512, 32768]."""
     import numpy as np
@@ -586,43 +636,154 @@ def bench_widened(torch, gk, dev):
     return res
 
 
-def cpu_baseline(max_seconds: float):
-    """BASELINE config 1 on the host with the C oracle (1 thread): single
-    sliding layer, 8x256 KV, 16 q heads, 1024-slot ring (page 1), sequential
-    append+attend steps from an empty cache; bounded to about `max_seconds`."""
+def _stats(values):
+    import statistics
+    return {"median": statistics.median(values), "min": min(values), "max": max(values),
+            "runs": len(values)}
+
+
+def _log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(runs_1core: int = 3, runs_all: int = 5, quick: bool = False):
+    """The oracle's append + decode attention timed in C on the host cores,
+    on one thread (the reference's own host reference is single-threaded)
+    and on a pool of all host threads split over (sequence, KV head) tasks.
+
+    Primary row: BASELINE config 1 in full -- one sliding layer, 8x256 KV, 16
+    q heads, 1024-slot page-1 ring, 2048 sequential append+attend steps from
+    an empty cache, N(0,1) inputs, scale 1/16 -- the 2048-step loop timed
+    inside C. One-step rows for configs 2 (48 layers, context 8192), 3 (64
+    sequences, contexts U[512, 32768], one global layer) and 4 (131072 keys,
+    1% x8). Reported per row: median / min / max seconds over the runs."""
     import numpy as np
     from oracle import oracle
-    rng = np.random.default_rng(1)
-    cfg = (1, WINDOW, 1, WINDOW, 1, HEADS, DIM, WINDOW)
-    ck = np.zeros(WINDOW * HEADS * DIM, np.uint16)
-    cv = np.zeros_like(ck)
-    pt = np.full(WINDOW, -1, np.int32)
-    slots = np.full(WINDOW, -1, np.int32)
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    threads = max(1, threads)
+    fill_threads = threads
     scale = 1.0 / 16.0
-    total_bytes = 0
-    steps = 0
-    t0 = time.perf_counter()
-    elapsed = 0.0
-    compute = 0.0
-    for step in range(2048):
-        q = oracle.f32_to_bf16(rng.standard_normal((1, QH, DIM), dtype=np.float32))
-        k = oracle.f32_to_bf16(rng.standard_normal((1, HEADS, DIM), dtype=np.float32))
-        v = oracle.f32_to_bf16(rng.standard_normal((1, HEADS, DIM), dtype=np.float32))
-        assert oracle.ensure_page(pt, slots, cfg, 0, step) >= 0
-        c0 = time.perf_counter()
-        oracle.kv_cache_write(ck, cv, cfg, pt, [0], [step], 0, k, v)
-        oracle.decode_attention(q, ck, cv, pt, [step + 1], cfg, 0, scale)
-        compute += time.perf_counter() - c0
-        total_bytes += layer_bytes(min(step + 1, WINDOW))
-        steps += 1
-        elapsed = time.perf_counter() - t0
-        if elapsed > max_seconds:
-            break
-    return {"value": total_bytes / compute / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "us_per_layer_step": compute / steps * 1e6, "steps": steps,
-            "sample": f"config1 steps 0..{steps - 1} of 2048 (ring 1024, 8x256 KV, 16 q heads), "
-                      f"C oracle -O3 single thread, append+attend per step, {compute:.1f} s",
-            "cpu_model": _cpu_model(), "host_threads": os.cpu_count()}
+    rows = {}
+
+    # ---- config 1: the full 2048-step loop.
+    steps = 256 if quick else 2048
+    q = oracle.fill_normal_bf16((steps, QH, DIM), 101, threads=fill_threads)
+    k = oracle.fill_normal_bf16((steps, HEADS, DIM), 102, threads=fill_threads)
+    v = oracle.fill_normal_bf16((steps, HEADS, DIM), 103, threads=fill_threads)
+    c1 = (1, WINDOW, 1, WINDOW, 1, HEADS, DIM, WINDOW)
+    c1_bytes = sum(layer_bytes(min(t + 1, WINDOW)) for t in range(steps))
+    ref_out = None
+    for name, th, runs in (("1core", 1, runs_1core), ("all_cores", threads, runs_all)):
+        secs = []
+        for r in range(runs):
+            _log(f"cpu config1 {name} run {r + 1}/{runs}")
+            sec, out, *_ = oracle.time_config1(q, k, v, c1, scale, th)
+            assert sec > 0
+            if ref_out is None:
+                ref_out = out
+            assert np.array_equal(out, ref_out), "threaded CPU run differs from 1-core run"
+            secs.append(sec)
+        st = _stats(secs)
+        rows[f"config1_{name}"] = {
+            "threads": min(th, HEADS),  # one task per KV head "seconds": st, "us_per_layer_step": st["median"] / steps * 1e6,
+            "GBs": c1_bytes / st["median"] / 1e9}
+    del q, k, v
+
+    # ---- one-step rows for configs 2-4 (caches filled once per config).
+    def fill_caches(cfgs):
+        """Seeded N(0,1) K and V caches for each config."""
+        rng_seed = 200
+        caches = []
+        for c in cfgs:
+            n = c[0] * c[1] * c[2] * c[5] * c[6]
+            caches.append((oracle.fill_normal_bf16((n,), rng_seed, threads=fill_threads),
+                           oracle.fill_normal_bf16((n,), rng_seed + 1, threads=fill_threads)))
+            rng_seed += 2
+        return caches
+
+    def run_rows(name, cfgs, pts, caches, layer_list, seq, pos, batch, bytes_per_step,
+                 runs_single):
+        """Time one step: for each (config index, cache layer) of layer_list,
+        the append + attention of `batch` sequences."""
+        q = oracle.fill_normal_bf16((batch, QH, DIM), 301, threads=fill_threads)
+        kn = oracle.fill_normal_bf16((batch, HEADS, DIM), 302, threads=fill_threads)
+        vn = oracle.fill_normal_bf16((batch, HEADS, DIM), 303, threads=fill_threads)
+        out = np.zeros_like(q)
+        for tag, th, runs in (("1core", 1, runs_single), ("all_cores", threads, runs_all)):
+            secs = []
+            for r in range(runs):
+                _log(f"cpu {name} {tag} run {r + 1}/{runs}")
+                total = 0.0
+                for ci, cl in layer_list:
+                    ck, cv = caches[ci]
+                    total += oracle.time_decode_layer(out, q, ck, cv, pts[ci], seq, pos, kn, vn,
+                                                      cfgs[ci], cl, scale, th)
+                secs.append(total)
+            st = _stats(secs)
+            rows[f"{name}_{tag}"] = {"threads": th, "seconds": st,
+                                     "us_per_layer_step": st["median"] / len(layer_list) * 1e6,
+                                     "GBs": bytes_per_step / st["median"] / 1e9}
+
+    # config 2: 48 layers, batch 1, context 8192 (+ the appended token).
+    seq_len = CONTEXT + 1
+    g_pages = (seq_len + GLOBAL_PAGE - 1) // GLOBAL_PAGE
+    s_cfg = (40, WINDOW, 1, WINDOW, 1, HEADS, DIM, WINDOW)
+    g_cfg = (8, g_pages, GLOBAL_PAGE, g_pages, 1, HEADS, DIM, 0)
+    caches = fill_caches((s_cfg, g_cfg))
+    pts = (np.arange(WINDOW, dtype=np.int32), np.arange(g_pages, dtype=np.int32))
+    layer_list, si, gi, c2_bytes = [], 0, 0, 0
+    for l in range(NUM_LAYERS):
+        if is_global_layer(l):
+            layer_list.append((1, gi)); gi += 1
+            c2_bytes += layer_bytes(seq_len)
+        else:
+            layer_list.append((0, si)); si += 1
+            c2_bytes += layer_bytes(WINDOW)
+    run_rows("config2_step", (s_cfg, g_cfg), pts, caches, layer_list,
+             np.array([seq_len], np.int32), np.array([CONTEXT], np.int32), 1, c2_bytes,
+             1 if quick else runs_1core)
+    del caches
+
+    if not quick:
+        # config 3: 64 sequences, contexts U[512, 32768] (the GPU leg's seed),
+        # pages allocated per sequence back to back.
+        rng = np.random.default_rng(64)
+        seq = rng.integers(512, 32769, size=64).astype(np.int32)
+        max_pages = (int(seq.max()) + GLOBAL_PAGE - 1) // GLOBAL_PAGE
+        need = (seq + GLOBAL_PAGE - 1) // GLOBAL_PAGE
+        pt = np.full(64 * max_pages, -1, np.int32)
+        nxt = 0
+        for b in range(64):
+            pt[b * max_pages: b * max_pages + need[b]] = np.arange(nxt, nxt + need[b])
+            nxt += int(need[b])
+        c3 = (1, nxt, GLOBAL_PAGE, max_pages, 64, HEADS, DIM, 0)
+        caches = fill_caches((c3,))
+        run_rows("config3_step", (c3,), (pt,), caches, [(0, 0)], seq, seq - 1, 64,
+                 sum(layer_bytes(int(s)) for s in seq), 1)
+        del caches
+
+        # config 4: 131072 keys, 1% of them x8.
+        ctx = 131072
+        c4 = (1, ctx // GLOBAL_PAGE, GLOBAL_PAGE, ctx // GLOBAL_PAGE, 1, HEADS, DIM, 0)
+        caches = fill_caches((c4,))
+        hot = np.random.default_rng(4).permutation(ctx)[:ctx // 100]
+        ck = caches[0][0].reshape(ctx, HEADS * DIM)
+        ck[hot] = oracle.f32_to_bf16(oracle.bf16_to_f32(ck[hot]) * 8)
+        run_rows("config4_step", (c4,), (np.arange(ctx // GLOBAL_PAGE, dtype=np.int32),), caches,
+                 [(0, 0)], np.array([ctx], np.int32), np.array([ctx - 1], np.int32), 1,
+                 layer_bytes(ctx), runs_1core)
+        del caches
+
+    head = rows["config1_all_cores"]
+    return {"value": round(head["GBs"], 3), "unit": "GB/s", "cores": head["threads"],
+            "kind": "port",
+            "us_per_layer_step": round(head["us_per_layer_step"], 1),
+            "sample": (f"config1 in full: {steps} sequential append+attend steps from an empty "
+                       f"1024-slot ring (8x256 KV, 16 q heads), the loop timed inside C; value = "
+                       f"median of {runs_all} runs on {min(threads, HEADS)} threads (one "
+                       f"task per KV head of the one sequence); 1-core and configs 2-4 one-step rows in 'rows'"),
+            "rows": rows, "cpu_model": _cpu_model(), "nproc": os.cpu_count(),
+            "threads_available": threads}
 
 
 def _cpu_model():
@@ -640,7 +801,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--cpu-quick", action="store_true",
+                    help="CPU baseline on a 256-step sample of config 1 and config 2 only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-batch64", action="store_true")
     ap.add_argument("--no-long", action="store_true")
@@ -791,6 +953,7 @@ def main():
                                  "algorithmic_bytes_per_launch": s_bytes,
                                  "split_size": s_layers[0].split, "num_splits": s_layers[0].n_splits},
     }
+    result["config1_gpu"] = bench_config1(torch, gk, dev)
     if not args.no_batch64:
         b64 = bench_batch64(torch, gk, dev, max(3, args.steps // 5), 2)
         result["batch64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in b64.items()}
@@ -804,7 +967,7 @@ def main():
     if not args.no_widened:
         result["widened"] = bench_widened(torch, gk, dev)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(quick=args.cpu_quick)
     print(json.dumps(result))
 
 

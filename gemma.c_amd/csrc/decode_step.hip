@@ -1,5 +1,5 @@
-// Persistent decode step for gfx950: one cooperative launch walks a run of
-// consecutive model layers, and for each layer appends the current token's
+// Persistent decode step for gfx950: one launch of one workgroup per CU walks
+// a run of consecutive model layers, and for each layer appends the current token's
 // K/V and runs split-K GQA decode attention with its log-sum-exp combine.
 // Replaces the per-layer launches of the reference decode loop
 // (src/gemma4_decode_megakernel.cu:172-183 calling
@@ -54,11 +54,17 @@
 //     next layer's q. Flags hold the launch epoch
 //     (1 + the value the previous launch left in the workspace header), so
 //     they never need clearing.
-// The XCD mapping needs exactly 32 workgroups per XCD; workspace
-// initialisation checks that once by a probe launch of this kernel and
-// otherwise reports the entry point unsupported.
-// Every wait is bounded by the real-time clock: on expiry the launch sets an
-// error bit, stops waiting and drains (results are then undefined).
+// The XCD mapping needs exactly 32 workgroups per XCD, one per CU;
+// workspace initialisation checks that once by a probe launch of this kernel
+// and otherwise reports the entry point unsupported.
+// Every wait is bounded by the real-time clock. The steps are ordinary
+// launches that rely on all 256 workgroups being resident together (each
+// takes a whole CU's LDS), which holds while no other kernel occupies CUs.
+// If a wait gives up, the wave stops waiting, writes zeros for the output
+// chunks it owns from that layer on, and records the error code and the
+// launch's epoch in the workspace header. The error is sticky: every later
+// launch on the workspace sees it at entry, writes zeros to all its outputs,
+// touches no cache and exits, until the workspace is initialised again.
 #include "gemma4_device.hpp"
 #include "decode_common.hpp"
 
@@ -98,8 +104,13 @@ constexpr int kXcds = 8;                      // XCDs of an MI355X
 constexpr int kXcdSlots = 32;                 // workgroups (CUs) per XCD
 constexpr int kMaxBatch = 8;                  // at least 4 splits per unit
 constexpr uint32_t kSentinel = 0x7fa5a5a5u;   // signalling NaN
-constexpr int kHeaderInts = 64;               // epoch, error, pad
-constexpr int kHeaderEpoch = 0, kHeaderError = 1;
+constexpr int kHeaderInts = 64;               // epoch, error, ..., pad
+// Header words: launch epoch; error code (0 ok, 1 a wait gave up, 2 a split
+// longer than the row tables); the epoch of the launch that set the error;
+// and a fault-injection hook for tests (stall layer + 1, its wait limit in
+// ticks, and a word the host never sets).
+constexpr int kHeaderEpoch = 0, kHeaderError = 1, kHeaderErrorEpoch = 2;
+constexpr int kHeaderStallLayer = 3, kHeaderStallTicks = 4, kHeaderNeverSet = 5;
 constexpr int kTicketStride = 32;             // ints between the XCD ticket counters
 constexpr int kGlobalFlagStride = 16;         // ints per layer: one flag per XCD
 constexpr uint64_t kWaitTicks = 100ull * 1000 * 1000 / 5;  // 0.2 s at 100 MHz
@@ -159,6 +170,13 @@ __device__ __forceinline__ uint32_t xcc_id() {
   asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
   return v;
 }
+// The CU this wave runs on within its XCD: HW_ID bits 8..15 (CU id, SH id,
+// SE id).
+__device__ __forceinline__ uint32_t hw_cu_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(v));
+  return (v >> 8) & 0xff;
+}
 // Reads of data another workgroup of the same XCD wrote with ordinary
 // stores. sc0|nt loads skip the CU's L1 (an sc0 load alone can still hit a
 // stale L1 line) and are served by the XCD's L2, clean or dirty, so a poll
@@ -208,6 +226,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   __shared__ uint4 s_q[kWave];    // q rows of the unit: [g][pack]
   __shared__ uint4 s_new[kWave];  // appended rows of the unit: [K pack | V pack]
   __shared__ int32_t s_ticket;
+  __shared__ int32_t s_failed;
   __shared__ int4 s_lds_rows[kLdsSlots * kTileKeys / 4];  // cache rows of the LDS tiles
   extern __shared__ uint4 s_tiles[];  // [slot][K 0..3 | V 0..3][lane]
 
@@ -215,7 +234,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   const int wave = wave_uniform(threadIdx.x / kWave);
   const int32_t xcd = (int32_t)(xcc_id() & 0xf);
   if (p.probe != nullptr) {
-    if (threadIdx.x == 0) p.probe[blockIdx.x] = xcd;
+    // XCD id and the CU's place in it (HW_ID bits 8..15: CU, SH, SE).
+    if (threadIdx.x == 0) p.probe[blockIdx.x] = xcd | (int32_t)(hw_cu_id() << 8);
     return;
   }
   if (threadIdx.x == kControlWave * kWave) {
@@ -223,6 +243,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     s_ticket = (int32_t)(__hip_atomic_fetch_add(p.tickets + xcd * kTicketStride, 1u,
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) %
                          kXcdSlots);
+    // A failed earlier launch (error recorded under another epoch) turns
+    // this launch into a no-op that writes zeros.
+    const int32_t err = coherent_load_i32(p.header + kHeaderError);
+    const int32_t err_epoch = coherent_load_i32(p.header + kHeaderErrorEpoch);
+    const int32_t ep = coherent_load_i32(p.header + kHeaderEpoch) + 1;
+    s_failed = err != 0 && err_epoch != ep;
   }
   __syncthreads();
   const int32_t ticket = wave_uniform(s_ticket);
@@ -242,6 +268,22 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   };
   const int32_t epoch = coherent_load_i32(p.header + kHeaderEpoch) + 1;
   auto is_global_i = [&](int32_t i) { return model_layer_global(p.first_layer + i); };
+  // Zeros for the output chunks this workgroup owns (those it combines:
+  // c = split, split + splits, ... of both rows of unit u), layers from..end.
+  auto zero_own_chunks = [&](int32_t from) {
+    const int g = lane >> 5;
+    const int32_t c = split + (lane & 31) * p.splits;
+    if (!active || c >= kChunks) return;
+    for (int32_t i = from; i < p.layer_count; ++i) {
+      uint4 *dst = reinterpret_cast<uint4 *>(p.out + i * q_stride + (u * kSGroup + g) * kSDim +
+                                             c * kPackElems);
+      *dst = make_uint4(0, 0, 0, 0);
+    }
+  };
+  if (wave_uniform(s_failed)) {
+    if (wave == kControlWave) zero_own_chunks(0);
+    return;
+  }
 
   // Wave-local tile j of a split is tile t = wave + 4 j; tiles 0..15 are
   // prefetched into compute-wave registers, tiles 16 .. 16 + kLdsSlots - 1
@@ -335,15 +377,27 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     // changed nothing).
     __builtin_amdgcn_s_setprio(3);
     bool abort = false;
+    // Records an error under this launch's epoch; a wait that gives up also
+    // stops every later wait of this wave.
+    auto fail = [&](int32_t code) {
+      abort = true;
+      if (lane == 0) {
+        coherent_store_i32(p.header + kHeaderErrorEpoch, epoch);
+        coherent_store_i32(p.header + kHeaderError, code);
+      }
+    };
     // A split longer than the row tables hold would drop keys: report it.
     for (int kind = 0; kind < 2; ++kind) {
       const Gemma4KvCacheConfig &c = p.c[kind];
       int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;
       first = first < 0 ? 0 : first;
       const int32_t n_keys = seq_len > first ? seq_len - first : 0;
-      if ((n_keys + p.splits - 1) / p.splits > kMaxSplitKeys && lane == 0)
-        coherent_store_i32(p.header + kHeaderError, 2);
+      if ((n_keys + p.splits - 1) / p.splits > kMaxSplitKeys) fail(2);
     }
+    // Fault injection for tests: at layer stall_layer - 1, ticket 0 of XCD 0
+    // waits, with the given limit, for a header word the host never sets.
+    const int32_t stall_layer = coherent_load_i32(p.header + kHeaderStallLayer) - 1;
+    const uint64_t stall_ticks = (uint32_t)coherent_load_i32(p.header + kHeaderStallTicks);
     // Layer `layer_i` is complete once all 8 XCD flags read `epoch`.
     auto wait_layer_device = [&](int32_t layer_i) {
       const int32_t *row = p.global_flags + layer_i * kGlobalFlagStride;
@@ -351,7 +405,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       while (!abort) {
         const bool ok = lane >= kXcds || coherent_load_i32(row + lane) == epoch;
         if (__ballot(!ok) == 0) break;
-        if (now_ticks() - t0 > kWaitTicks) abort = true;
+        if (now_ticks() - t0 > kWaitTicks) fail(1);
       }
     };
     // Ticket 0 of each XCD polls the 8 device flags and raises the XCD's
@@ -369,7 +423,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       while (!abort) {
         const int32_t v = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(go_buf, off, 0, kLocalLoadAux);
         if (v == epoch) break;
-        if (now_ticks() - t0 > kWaitTicks) abort = true;
+        if (now_ticks() - t0 > kWaitTicks) fail(1);
       }
     };
     // Ticket 0 of each XCD: collect the XCD's 32 local flags, then raise
@@ -384,7 +438,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                         (int32_t)__builtin_amdgcn_raw_buffer_load_b32(local_buf, off, 0,
                                                                       kLocalLoadAux) == epoch;
         if (__ballot(!ok) == 0) break;
-        if (now_ticks() - t0 > kWaitTicks) abort = true;
+        if (now_ticks() - t0 > kWaitTicks) fail(1);
       }
       if (lane == 0) coherent_store_i32(p.global_flags + layer_i * kGlobalFlagStride + xcd, epoch);
     };
@@ -399,6 +453,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     const BufferRsrc in_buf_v = buffer_of(p.new_v, (int64_t)p.layer_count * kv_stride * 2);
     for (int32_t i = 0; i < p.layer_count; ++i) {
       if (i > 0) wait_layer(i - 1);
+      if (i == stall_layer && xcd == 0 && ticket == 0) {
+        const uint64_t t0 = now_ticks();
+        while (!abort && coherent_load_i32(p.header + kHeaderNeverSet) != epoch) {
+          if (now_ticks() - t0 > stall_ticks) fail(1);
+        }
+      }
       // Layer i's inputs exist only now: q rows and appended K/V rows of the
       // unit, read device-coherently and staged in LDS for the compute waves.
       {
@@ -443,7 +503,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
           const uint64_t t0 = now_ticks();
           issue(got);
           while (!complete(got) && !abort) {
-            if (now_ticks() - t0 > kWaitTicks) abort = true;
+            if (now_ticks() - t0 > kWaitTicks) fail(1);
             issue(got);
           }
         }
@@ -479,8 +539,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
             const float inv = big_l > 0.0f ? 1.0f / big_l : 0.0f;
             // Output rows go out device-coherent.
             const BufferRsrc out_buf = buffer_of(p.out + i * q_stride, q_stride * 2);
+            // After a wait gave up, this wave's chunks are written as zeros.
             __builtin_amdgcn_raw_buffer_store_b16(
-                (uint16_t)f32_to_bf16_bits(v[0] * inv), out_buf,
+                abort ? (uint16_t)0 : (uint16_t)f32_to_bf16_bits(v[0] * inv), out_buf,
                 ((u * kSGroup + g) * kSDim + c * kPackElems + dim) * 2, 0, kCoherentAux);
           }
         }
@@ -508,7 +569,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       wait_layer(p.layer_count - 1);
       if (lane == 0) coherent_store_i32(p.header + kHeaderEpoch, epoch);
     }
-    if (abort && lane == 0) coherent_store_i32(p.header + kHeaderError, 1);
+    // Another workgroup's wait gave up during this launch: zero the chunks
+    // this one wrote as well (best effort: it sees the error only if it was
+    // recorded before this point; the status word is the contract).
+    if (coherent_load_i32(p.header + kHeaderError) != 0 &&
+        coherent_load_i32(p.header + kHeaderErrorEpoch) == epoch)
+      zero_own_chunks(0);
     return;
   }
 
@@ -874,23 +940,27 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
   return p;
 }
 
-// The placement probe at workspace initialisation is a cooperative launch:
-// it checks that all 256 workgroups are resident together, one per CU and 32
-// per XCD (the 157 KB of LDS a workgroup takes leaves room for no second
-// one on a CU). The steps themselves are ordinary launches: a cooperative
-// launch costs ~18 us more per step to dispatch (405 vs 387 us per config-2
-// step), and on a GPU the step has to itself every workgroup is resident
-// anyway. Should another kernel hold CUs during a step, the bounded waits
-// expire and the status reports it; nothing hangs.
-hipError_t launch_step(StepParams &p, hipStream_t stream, bool cooperative) {
+// Every launch of the step kernel, the placement probe at workspace
+// initialisation included, is an ordinary launch. The probe checks that the
+// 256 workgroups land 32 per XCD on 256 distinct CUs (the 157 KB of LDS a
+// workgroup takes leaves room for no second one on a CU). A cooperative
+// launch is not used: it costs ~18 us more per step to dispatch (405 vs
+// 387 us per config-2 step), and HIP serves it from a dedicated queue whose
+// teardown at process exit crashed every profiled run that had made one.
+// Should another kernel hold CUs during a step, the bounded waits give up
+// and the error is recorded in the workspace header; nothing hangs.
+hipError_t launch_step(StepParams &p, hipStream_t stream) {
   void *args[] = {&p};
-  if (!cooperative) {
-    return hipLaunchKernel(reinterpret_cast<const void *>(decode_step_kernel),
-                           dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds, stream);
+  return hipLaunchKernel(reinterpret_cast<const void *>(decode_step_kernel),
+                         dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds, stream);
+}
+
+__global__ void decode_step_set_stall_kernel(int32_t *header, int32_t stall_layer_plus1,
+                                             int32_t ticks) {
+  if (threadIdx.x == 0) {
+    header[kHeaderStallLayer] = stall_layer_plus1;
+    header[kHeaderStallTicks] = ticks;
   }
-  return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(decode_step_kernel),
-                                    dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds,
-                                    stream);
 }
 
 bool step_geometry_ok(const Gemma4KvCacheConfig &c, int32_t batch_count) {
@@ -927,20 +997,26 @@ extern "C" hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t 
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPadLds);
     if (e != hipSuccess) return e;
     // One probe launch of the step kernel: every XCD must receive exactly
-    // 32 of its workgroups (one per CU) for the XCD-local exchange.
+    // 32 of its workgroups, on 32 distinct CUs, for the XCD-local exchange.
     StepParams p = base_params(workspace, w, batch_count);
     p.probe = ints + w.probe;
-    e = launch_step(p, stream, /*cooperative=*/true);
+    e = launch_step(p, stream);
     if (e != hipSuccess) return e;
     int32_t ids[kStepWorkgroups];
     e = hipMemcpyAsync(ids, p.probe, sizeof(ids), hipMemcpyDeviceToHost, stream);
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return e;
     int count[16] = {};
+    bool seen[kXcds][256] = {};
     bool ok = true;
     for (int32_t id : ids) {
-      if (id < 0 || id >= kXcds) ok = false;
-      else ++count[id];
+      const int32_t x = id & 0xff, cu = (id >> 8) & 0xff;
+      if (x >= kXcds || seen[x][cu]) {
+        ok = false;
+        continue;
+      }
+      seen[x][cu] = true;
+      ++count[x];
     }
     for (int x = 0; x < kXcds; ++x) ok &= count[x] == kXcdSlots;
     g_placement_ok[device] = ok ? 1 : -1;
@@ -953,8 +1029,25 @@ extern "C" hipError_t gemma4_decode_step_status(const void *workspace, int32_t *
   int32_t header[2] = {0, 0};
   const hipError_t e = hipMemcpy(header, workspace, sizeof(header), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return e;
-  *status = header[1];
+  *status = header[kHeaderError];
   return hipSuccess;
+}
+
+extern "C" hipError_t gemma4_decode_step_status_async(const void *workspace, int32_t *status,
+                                                      hipStream_t stream) {
+  if (workspace == nullptr || status == nullptr) return hipErrorInvalidValue;
+  return hipMemcpyAsync(status, static_cast<const int32_t *>(workspace) + kHeaderError,
+                        sizeof(int32_t), hipMemcpyDefault, stream);
+}
+
+extern "C" hipError_t gemma4_decode_step_inject_stall(void *workspace, int32_t layer,
+                                                      uint32_t limit_ticks, hipStream_t stream) {
+  if (workspace == nullptr || layer < -1 || layer >= kNumModelLayers ||
+      limit_ticks > 0x7fffffffu)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(decode_step_set_stall_kernel, 1, 64, 0, stream,
+                     static_cast<int32_t *>(workspace), layer + 1, (int32_t)limit_ticks);
+  return hipGetLastError();
 }
 
 extern "C" hipError_t gemma4_decode_step_layers_bf16(
@@ -1012,5 +1105,5 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
   p.first_layer = first_layer;
   p.layer_count = layer_count;
   p.q_scale = scale * kLog2e;
-  return launch_step(p, stream, /*cooperative=*/false);
+  return launch_step(p, stream);
 }

@@ -106,6 +106,8 @@ SIGNATURES = {
     "gemma4_decode_step_workspace_bytes": (ctypes.c_size_t, [_I32]),
     "gemma4_decode_step_workspace_init": (_I32, [_P, ctypes.c_size_t, _I32, _P]),
     "gemma4_decode_step_status": (_I32, [_P, ctypes.POINTER(_I32)]),
+    "gemma4_decode_step_status_async": (_I32, [_P, _P, _P]),
+    "gemma4_decode_step_inject_stall": (_I32, [_P, _I32, ctypes.c_uint32, _P]),
     "gemma4_decode_step_layers_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _CFG, _P, _P, _P, _CFG, _P, _P, _I32, _I32, _F32,
                _I32, _P, ctypes.c_size_t, _P]),
@@ -285,6 +287,18 @@ def decode_step_status(workspace) -> int:
     check(lib().gemma4_decode_step_status(ptr(workspace), ctypes.byref(st)),
           "gemma4_decode_step_status")
     return st.value
+
+
+def decode_step_status_async(workspace, status, stream=None) -> int:
+    """Stream-ordered copy of the step status word into `status` (a device
+    or pinned-host int32 tensor)."""
+    return lib().gemma4_decode_step_status_async(ptr(workspace), ptr(status),
+                                                 stream_handle(stream))
+
+
+def decode_step_inject_stall(workspace, layer: int, limit_ticks: int, stream=None) -> int:
+    return lib().gemma4_decode_step_inject_stall(ptr(workspace), layer, limit_ticks,
+                                                 stream_handle(stream))
 
 
 def decode_step_layers_bf16(out, q, k, v, sliding_k, sliding_v, sliding_page_table,

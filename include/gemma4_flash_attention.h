@@ -194,33 +194,52 @@ hipError_t gemma4_decode_prep_append_bf16(
     const float *sin, int32_t batch_count, hipStream_t stream);
 
 // ---- persistent decode step over consecutive layers --------------------
-// One persistent launch (256 workgroups, one per CU, all resident together:
-// the GPU must not run other kernels during the step) that runs, for model
-// layers first_layer ..
-// first_layer + layer_count - 1 in order, the fused K/V append of the current
-// token and the split-K decode attention with its combine, for `batch_count`
-// sequences. Replaces the per-layer attention launches of the reference
-// decode loop (src/gemma4_decode_megakernel.cu:172-183 ->
-// gemma4_decode_megakernel_flash_attention_layer_bf16, append + attention
+// One persistent launch (an ordinary launch of 256 workgroups, one per CU;
+// it relies on all of them being resident together, which holds while no
+// other kernel occupies CUs during the step) that runs, for model layers
+// first_layer .. first_layer + layer_count - 1 in order, the fused K/V
+// append of the current token and the split-K decode attention with its
+// combine, for `batch_count` sequences. Replaces the per-layer attention
+// launches of the reference decode loop (src/gemma4_decode_megakernel.cu:172-183
+// -> gemma4_decode_megakernel_flash_attention_layer_bf16, append + attention
 // phases src/gemma4_flash_attention_decode.cu:979-1067).
 //   q, out: [layer_count][batch_count][16][256] bf16; k, v (the appended
 //   rows): [layer_count][batch_count][8][256]. Layer i reads q/k/v[i] only
 //   after out[i-1] is complete (the order a real decode step imposes).
 //   Sliding layers use the sliding cache/config/page table, global layers
 //   (every 6th and the last) the global ones; both geometries must be 8 KV
-//   heads x 256. seq_lengths / token_position: as for the per-layer entry
-//   points (one step: the same for every layer).
+//   heads x 256 (the reference model's 1 x 512 global geometry is served by
+//   the per-layer entry points). seq_lengths / token_position: as for the
+//   per-layer entry points (one step: the same for every layer).
 // `workspace` (gemma4_decode_step_workspace_bytes bytes) holds the split
 // records and layer flags; initialise it once with
-// gemma4_decode_step_workspace_init, then reuse it for every step (stream
-// order). Calls sharing a workspace must not overlap. After a call,
-// gemma4_decode_step_status reports 0, or a nonzero code if a bounded wait
-// expired (1, e.g. another kernel held CUs; the workspace must then be
-// initialised again) or a split exceeded the 512-key table (2).
+// gemma4_decode_step_workspace_init (which also checks, once per device,
+// that the workgroups land one per CU, 32 per XCD; hipErrorNotSupported
+// otherwise), then reuse it for every step (stream order). Calls sharing a
+// workspace must not overlap.
+// Failure is stream-ordered and sticky: every wait of the step is bounded
+// (0.2 s); if one gives up (another kernel held CUs), the launch writes
+// zeros for the output chunks whose wait gave up and records a nonzero
+// status in the workspace; every later launch on that workspace then writes
+// zeros to all of its outputs, appends nothing and returns at once, until
+// gemma4_decode_step_workspace_init is called again. Status codes: 0 ok, 1 a
+// wait gave up, 2 a split exceeded the 512-key row table.
+// gemma4_decode_step_status reads it synchronously;
+// gemma4_decode_step_status_async copies it (4 bytes) to `status` (host
+// pinned or device memory) in stream order.
 size_t gemma4_decode_step_workspace_bytes(int32_t batch_count);
 hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t workspace_bytes,
                                              int32_t batch_count, hipStream_t stream);
 hipError_t gemma4_decode_step_status(const void *workspace, int32_t *status);
+hipError_t gemma4_decode_step_status_async(const void *workspace, int32_t *status,
+                                           hipStream_t stream);
+// Fault injection for tests (no counterpart in the reference): from the next
+// launch on, at launch-relative layer `layer` one workgroup waits for a
+// workspace word that is never set, giving up after `limit_ticks` of the
+// 100 MHz real-time clock, so a failed step can be produced without holding
+// CUs. layer -1 switches it off; workspace_init clears it.
+hipError_t gemma4_decode_step_inject_stall(void *workspace, int32_t layer,
+                                           uint32_t limit_ticks, hipStream_t stream);
 hipError_t gemma4_decode_step_layers_bf16(
     gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
     gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,

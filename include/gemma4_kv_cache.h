@@ -23,6 +23,11 @@ typedef uint16_t gemma4_bf16;  // C callers pass raw bf16 bit patterns
 #else
 #define GEMMA4_HOST_DEVICE
 #endif
+#ifdef __cplusplus
+#define GEMMA4_CONSTEXPR constexpr
+#else
+#define GEMMA4_CONSTEXPR
+#endif
 
 // Replaces src/gemma4_kv_cache.cuh:9-18 (same 8 x int32 layout, 32 bytes).
 // window_size == 0 marks a full-length global cache; > 0 a sliding ring.
@@ -38,8 +43,9 @@ typedef struct Gemma4KvCacheConfig {
 } Gemma4KvCacheConfig;
 
 // Replaces src/gemma4_kv_cache.cuh:27-38. Flat Layout-A element offset
-// [layer][page][page_offset][head][dim].
-static inline GEMMA4_HOST_DEVICE int64_t gemma4_kv_cache_offset(
+// [layer][page][page_offset][head][dim]; constexpr in C++ (usable in
+// constant expressions, as the reference's is).
+static inline GEMMA4_CONSTEXPR GEMMA4_HOST_DEVICE int64_t gemma4_kv_cache_offset(
     const Gemma4KvCacheConfig *config, int32_t layer, int32_t page,
     int32_t page_offset, int32_t head, int32_t dim) {
   const int64_t layer_page = (int64_t)layer * config->num_pages + page;
@@ -48,8 +54,9 @@ static inline GEMMA4_HOST_DEVICE int64_t gemma4_kv_cache_offset(
 }
 
 #ifdef __cplusplus
-// Reference-style overload taking the config by reference.
-static inline GEMMA4_HOST_DEVICE int64_t gemma4_kv_cache_offset(
+// Reference-style overload taking the config by reference
+// (src/gemma4_kv_cache.cuh:28, __host__ __device__ constexpr).
+static inline constexpr GEMMA4_HOST_DEVICE int64_t gemma4_kv_cache_offset(
     const Gemma4KvCacheConfig &config, int32_t layer, int32_t page,
     int32_t page_offset, int32_t head, int32_t dim) {
   return gemma4_kv_cache_offset(&config, layer, page, page_offset, head, dim);

@@ -188,7 +188,56 @@ static void live_key_range(const OracleKvCacheConfig *c, int32_t seq_len,
  * reference host attention (tests/test_flash_attention.cu:124-172) applied to
  * the last query row, with keys gathered through the page table and the
  * sliding window counting the current token (src/gemma4.h:22-23,
- * src/gemma4_flash_attention_decode.cu:730-732). */
+ * src/gemma4_flash_attention_decode.cu:730-732). One (sequence, query head)
+ * row; the scratch buffers hold head_dim floats (qf, acc) and seq_len
+ * entries (scores, rows). */
+void oracle_decode_attention_row(uint16_t *out, const uint16_t *q,
+                                 const uint16_t *cache_k, const uint16_t *cache_v,
+                                 const int32_t *page_table, int32_t seq_len,
+                                 const OracleKvCacheConfig *c, int32_t layer,
+                                 float softmax_scale, int32_t b, int32_t qh,
+                                 int32_t q_heads, float *qf, float *acc,
+                                 float *scores, int64_t *rows) {
+  const int32_t D = c->head_dim;
+  const int32_t group = q_heads / c->num_heads;
+  int32_t first, count;
+  live_key_range(c, seq_len, &first, &count);
+  const int32_t kvh = qh / group;
+  const int64_t q_base = ((int64_t)b * q_heads + qh) * D;
+  for (int32_t d = 0; d < D; ++d) qf[d] = oracle_bf16_to_f32(q[q_base + d]);
+  int32_t n = 0;
+  float max_score = -INFINITY;
+  for (int32_t i = 0; i < count; ++i) {
+    const int32_t pos = first + i;
+    const int32_t phys = key_physical_page(c, page_table, b, pos);
+    if (phys < 0) continue;
+    const int64_t row = oracle_kv_cache_offset(c, layer, phys, pos % c->page_size, kvh, 0);
+    float score = 0.0f;
+    for (int32_t d = 0; d < D; ++d) {
+      score += qf[d] * oracle_bf16_to_f32(cache_k[row + d]);
+    }
+    score *= softmax_scale;
+    rows[n] = row;
+    scores[n] = score;
+    if (score > max_score) max_score = score;
+    ++n;
+  }
+  float denom = 0.0f;
+  for (int32_t i = 0; i < n; ++i) {
+    scores[i] = expf(scores[i] - max_score);
+    denom += scores[i];
+  }
+  for (int32_t d = 0; d < D; ++d) acc[d] = 0.0f;
+  for (int32_t i = 0; i < n; ++i) {
+    const float w = scores[i] / denom;
+    const uint16_t *vrow = cache_v + rows[i];
+    for (int32_t d = 0; d < D; ++d) acc[d] += w * oracle_bf16_to_f32(vrow[d]);
+  }
+  for (int32_t d = 0; d < D; ++d) {
+    out[q_base + d] = oracle_f32_to_bf16(n > 0 ? acc[d] : 0.0f);
+  }
+}
+
 void oracle_decode_attention(uint16_t *out, const uint16_t *q,
                              const uint16_t *cache_k, const uint16_t *cache_v,
                              const int32_t *page_table,
@@ -197,55 +246,19 @@ void oracle_decode_attention(uint16_t *out, const uint16_t *q,
                              float softmax_scale, int32_t batch_count,
                              int32_t q_heads) {
   const int32_t D = c->head_dim;
-  const int32_t group = q_heads / c->num_heads;
-  float *qf = (float *)malloc(sizeof(float) * D);
-  float *acc = (float *)malloc(sizeof(float) * D);
   int32_t max_keys = 0;
   for (int32_t b = 0; b < batch_count; ++b) {
     if (seq_lengths[b] > max_keys) max_keys = seq_lengths[b];
   }
-  float *scores = (float *)malloc(sizeof(float) * (max_keys > 0 ? max_keys : 1));
-  int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * (max_keys > 0 ? max_keys : 1));
-
+  const int32_t cap = max_keys > 0 ? max_keys : 1;
+  float *qf = (float *)malloc(sizeof(float) * D);
+  float *acc = (float *)malloc(sizeof(float) * D);
+  float *scores = (float *)malloc(sizeof(float) * cap);
+  int64_t *rows = (int64_t *)malloc(sizeof(int64_t) * cap);
   for (int32_t b = 0; b < batch_count; ++b) {
-    int32_t first, count;
-    live_key_range(c, seq_lengths[b], &first, &count);
     for (int32_t qh = 0; qh < q_heads; ++qh) {
-      const int32_t kvh = qh / group;
-      const int64_t q_base = ((int64_t)b * q_heads + qh) * D;
-      for (int32_t d = 0; d < D; ++d) qf[d] = oracle_bf16_to_f32(q[q_base + d]);
-      int32_t n = 0;
-      float max_score = -INFINITY;
-      for (int32_t i = 0; i < count; ++i) {
-        const int32_t pos = first + i;
-        const int32_t phys = key_physical_page(c, page_table, b, pos);
-        if (phys < 0) continue;
-        const int64_t row = oracle_kv_cache_offset(
-            c, layer, phys, pos % c->page_size, kvh, 0);
-        float score = 0.0f;
-        for (int32_t d = 0; d < D; ++d) {
-          score += qf[d] * oracle_bf16_to_f32(cache_k[row + d]);
-        }
-        score *= softmax_scale;
-        rows[n] = row;
-        scores[n] = score;
-        if (score > max_score) max_score = score;
-        ++n;
-      }
-      float denom = 0.0f;
-      for (int32_t i = 0; i < n; ++i) {
-        scores[i] = expf(scores[i] - max_score);
-        denom += scores[i];
-      }
-      for (int32_t d = 0; d < D; ++d) acc[d] = 0.0f;
-      for (int32_t i = 0; i < n; ++i) {
-        const float w = scores[i] / denom;
-        const uint16_t *vrow = cache_v + rows[i];
-        for (int32_t d = 0; d < D; ++d) acc[d] += w * oracle_bf16_to_f32(vrow[d]);
-      }
-      for (int32_t d = 0; d < D; ++d) {
-        out[q_base + d] = oracle_f32_to_bf16(n > 0 ? acc[d] : 0.0f);
-      }
+      oracle_decode_attention_row(out, q, cache_k, cache_v, page_table, seq_lengths[b], c,
+                                  layer, softmax_scale, b, qh, q_heads, qf, acc, scores, rows);
     }
   }
   free(qf);

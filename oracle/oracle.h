@@ -94,6 +94,16 @@ void oracle_decode_attention(uint16_t *out, const uint16_t *q,
                              float softmax_scale, int32_t batch_count,
                              int32_t q_heads);
 
+/* One (sequence b, query head qh) row of oracle_decode_attention; scratch:
+ * qf, acc hold head_dim floats, scores/rows hold seq_len entries. */
+void oracle_decode_attention_row(uint16_t *out, const uint16_t *q,
+                                 const uint16_t *cache_k, const uint16_t *cache_v,
+                                 const int32_t *page_table, int32_t seq_len,
+                                 const OracleKvCacheConfig *config, int32_t layer,
+                                 float softmax_scale, int32_t b, int32_t qh,
+                                 int32_t q_heads, float *qf, float *acc,
+                                 float *scores, int64_t *rows);
+
 /* Split-K partials (online update per key) and the log-sum-exp combine. */
 void oracle_decode_split(float *partial_m, float *partial_l,
                          float *partial_acc, const uint16_t *q,
@@ -134,6 +144,24 @@ void oracle_attention_o_projection(uint16_t *residual_out, uint16_t *normed_out,
 void oracle_fill_rope_tables(float *cos_table, float *sin_table,
                              int32_t max_seq_len, int32_t rotary_half,
                              float theta, int32_t exponent_dim);
+
+/* CPU baseline timings (oracle/cpu_baseline.c): the oracle's append and
+ * decode attention timed on 1 or more host threads, split over (sequence,
+ * KV head) tasks. Return seconds of compute (inputs generated beforehand). */
+void oracle_fill_normal_bf16(uint16_t *dst, int64_t n, uint64_t seed, float scale,
+                             int32_t threads);
+double oracle_time_decode_layer(uint16_t *out, const uint16_t *q, uint16_t *cache_k,
+                                uint16_t *cache_v, const int32_t *page_table,
+                                const int32_t *seq_lengths, const int32_t *token_position,
+                                const uint16_t *k_new, const uint16_t *v_new,
+                                const OracleKvCacheConfig *config, int32_t layer,
+                                float scale, int32_t batch, int32_t q_heads,
+                                int32_t threads);
+double oracle_time_config1(uint16_t *out, const uint16_t *q, const uint16_t *k,
+                           const uint16_t *v, uint16_t *cache_k, uint16_t *cache_v,
+                           int32_t *page_table, int32_t *slot_logical_pages,
+                           const OracleKvCacheConfig *config, float scale, int32_t steps,
+                           int32_t q_heads, int32_t threads);
 
 #ifdef __cplusplus
 }

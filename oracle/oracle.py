@@ -61,6 +61,10 @@ def lib():
             "oracle_attention_o_projection": (None, [P, P, P, P, P, P, P, I, I, I, F]),
             "oracle_f32_to_bf16_array": (None, [P, P, ctypes.c_int64]),
             "oracle_bf16_to_f32_array": (None, [P, P, ctypes.c_int64]),
+            "oracle_fill_normal_bf16": (None, [P, ctypes.c_int64, ctypes.c_uint64, F, I]),
+            "oracle_time_decode_layer": (ctypes.c_double,
+                                         [P, P, P, P, P, P, P, P, P, C, I, F, I, I, I]),
+            "oracle_time_config1": (ctypes.c_double, [P, P, P, P, P, P, P, P, C, F, I, I, I]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(_lib, name)
@@ -231,3 +235,43 @@ def attention_o_projection(attn, w_col_major, norm_weight, x, eps=1e-6):
     lib().oracle_attention_o_projection(*(_p(o) for o in outs), _p(attn), _p(w), _p(g), _p(x),
                                         rows, width, hidden, eps)
     return tuple(outs)
+
+
+# ---- CPU baseline timings (cpu_baseline.c) --------------------------------
+
+def fill_normal_bf16(shape, seed, scale=1.0, threads=1) -> np.ndarray:
+    """Seeded N(0,1)*scale bf16 array; values independent of `threads`."""
+    out = np.empty(shape, dtype=np.uint16)
+    lib().oracle_fill_normal_bf16(_p(out), out.size, seed, scale, threads)
+    return out
+
+
+def time_decode_layer(out, q, cache_k, cache_v, page_table, seq_lengths, token_position,
+                      k_new, v_new, c, layer, scale, threads, q_heads=16) -> float:
+    """Append + decode attention of one layer-step for len(seq_lengths)
+    sequences, timed in C; writes `out` and the caches in place."""
+    cc = cfg(c)
+    sl = np.ascontiguousarray(seq_lengths, dtype=np.int32)
+    tp = np.ascontiguousarray(token_position, dtype=np.int32)
+    pt = np.ascontiguousarray(page_table, dtype=np.int32)
+    return lib().oracle_time_decode_layer(_p(out), _p(q), _p(cache_k), _p(cache_v), _p(pt),
+                                          _p(sl), _p(tp), _p(k_new), _p(v_new), ctypes.byref(cc),
+                                          layer, scale, sl.size, q_heads, threads)
+
+
+def time_config1(q, k, v, c, scale, threads, q_heads=16):
+    """The config-1 loop (ensure_page, append, attend per step) from an empty
+    ring, timed in C. Returns (seconds, out [steps][q_heads][head_dim],
+    cache_k, cache_v, page_table)."""
+    cc = cfg(c)
+    steps = q.shape[0]
+    rows = cc.num_layers * cc.num_pages * cc.page_size * cc.num_heads * cc.head_dim
+    ck = np.zeros(rows, np.uint16)
+    cv = np.zeros(rows, np.uint16)
+    pt = np.full(cc.batch_size * cc.max_pages_per_seq, -1, np.int32)
+    slots = np.full(cc.batch_size * cc.max_pages_per_seq, -1, np.int32)
+    out = np.zeros((steps, q_heads, cc.head_dim), np.uint16)
+    sec = lib().oracle_time_config1(_p(out), _p(np.ascontiguousarray(q)), _p(np.ascontiguousarray(k)),
+                                    _p(np.ascontiguousarray(v)), _p(ck), _p(cv), _p(pt), _p(slots),
+                                    ctypes.byref(cc), scale, steps, q_heads, threads)
+    return sec, out, ck, cv, pt

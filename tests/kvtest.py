@@ -116,3 +116,16 @@ def torch_decode_reference(q_bits_t, cache_k_t, cache_v_t, page_table, seq_lengt
         o = torch.einsum("hgn,nhd->hgd", p, v).reshape(16, dim)
         outs.append(o)
     return torch.stack(outs)
+
+
+def device_i16(ptr: int, count: int, dev):
+    """Copy `count` int16 (bf16 bit patterns) from a raw device address that
+    the library owns (e.g. a runtime cache) into a new tensor."""
+    import ctypes
+    import torch
+    out = torch.empty(count, dtype=torch.int16, device=dev)
+    hip = ctypes.CDLL("libamdhip64.so.7")  # the runtime torch already loaded (same soname)
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(out.data_ptr(), ptr, count * 2, 3) == 0  # device to device
+    torch.cuda.synchronize()
+    return out

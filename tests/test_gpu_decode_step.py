@@ -68,10 +68,12 @@ def _expected(layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v, seq, pos, scale
     return exp, np.stack(outs)
 
 
-def _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos, scale):
+def _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos, scale,
+              expect_status=0, fill=0):
     import torch
     batch = len(seq)
     out = empty_bf16((len(layers), batch, 16, DIM), dev)
+    out.fill_(fill)
     code = gk.decode_step_layers_bf16(
         out, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), dcaches["sk"], dcaches["sv"],
         to_dev(s_pt, dev), gk.make_config(*s_cfg), dcaches["gk"], dcaches["gv"],
@@ -79,7 +81,7 @@ def _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, 
         to_dev(np.asarray(pos, np.int32), dev), layers[0], len(layers), scale, batch, ws)
     gk.check(code, "decode_step")
     torch.cuda.synchronize()
-    assert gk.decode_step_status(ws) == 0
+    assert gk.decode_step_status(ws) == expect_status
     return from_dev_bf16(out)
 
 
@@ -117,6 +119,53 @@ def test_decode_step_against_oracle(dev, first, count, seq, window, s_page, g_pa
     again = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos,
                       scale)
     assert np.array_equal(again, got)
+
+
+def test_decode_step_failure_is_reported_and_sticky(dev):
+    """A bounded wait made to give up from the host (fault injection: at layer
+    2 one workgroup waits for a word nothing sets, limit 20 us) while every
+    kernel still exits normally. The launch reports status 1 (synchronous and
+    stream-ordered reads agree) and the stalled workgroup's output chunk is
+    zero in every layer; the next launch on the workspace writes only zeros
+    and leaves the caches untouched; after workspace_init the same step is
+    correct again."""
+    import torch
+    rng = np.random.default_rng(99)
+    seq, first, count = [151], 0, 6
+    layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v = _case(rng, first, count, seq, 64, 1, 16)
+    pos = [n - 1 for n in seq]
+    scale = 1 / math.sqrt(DIM)
+    exp_caches, exp_out = _expected(layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v, seq,
+                                    pos, scale)
+    dcaches = {n: to_dev(a, dev) for n, a in caches.items()}
+    ws = _workspace(dev, 1)
+    gk.check(gk.decode_step_inject_stall(ws, 2, 2000), "inject_stall")
+    print("decode step: stalled launch", flush=True)
+    got1 = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos,
+                     scale, expect_status=1, fill=0x1234)
+    pinned = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+    gk.check(gk.decode_step_status_async(ws, pinned), "status_async")
+    torch.cuda.synchronize()
+    assert int(pinned[0]) == 1
+    # XCD 0, ticket 0 serves KV head 0, split 0: it combines output chunk 0
+    # (dims 0..7) of query heads 0 and 1.
+    assert not got1[:, 0, 0:2, 0:8].any()
+    snap = {n: t.clone() for n, t in dcaches.items()}
+    print("decode step: launch on the failed workspace", flush=True)
+    got2 = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos,
+                     scale, expect_status=1, fill=0x1234)
+    assert not got2.any()
+    for n in dcaches:
+        assert torch.equal(dcaches[n], snap[n]), n
+    # Re-initialised: the stall is cleared and the step is correct again.
+    gk.check(gk.decode_step_workspace_init(ws, 1), "workspace_init")
+    got3 = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq, pos,
+                     scale)
+    for n in caches:
+        assert np.array_equal(from_dev_bf16(dcaches[n]).reshape(caches[n].shape),
+                              exp_caches[n]), n
+    for i, layer in enumerate(layers):
+        assert_close(got3[i], exp_out[i], f"layer {layer}")
 
 
 def test_decode_step_rejects_bad_arguments(dev):
