@@ -415,7 +415,7 @@ def bench_batch64(torch, gk, dev, steps, warmup):
     return {"workload": "config3: 1 global layer, 64 seqs, ctx U[512,32768] seed 64",
             "us_per_layer_step": ms * 1e3, "achieved_GBs": gbs,
             "frac_of_peak": gbs / HBM_PEAK_GBS, "split_size": split, "num_splits": n,
-            "bytes_per_step": total}
+            "bytes_per_step": total, "traffic": read_traffic("decode_batch64_config3")}
 
 
 def bench_long(torch, gk, dev, steps, warmup, target_workgroups=0, counters=False, ctx=131072):
@@ -463,7 +463,8 @@ def bench_long(torch, gk, dev, steps, warmup, target_workgroups=0, counters=Fals
     return {"workload": "config4: 1 global layer, 1 seq, ctx 131072, 1% keys x8",
             "us_per_layer_step": ms * 1e3, "achieved_GBs": gbs,
             "frac_of_peak": gbs / HBM_PEAK_GBS, "split_size": split, "num_splits": n,
-            "in_kernel_combine": counters, "bytes_per_step": total}
+            "in_kernel_combine": counters, "bytes_per_step": total,
+            "traffic": read_traffic("decode_long_context_config4")}
 
 
 def bench_oproj(torch, gk, dev, rnd, rows_list=(1, 4, 8, 16, 64)):
@@ -685,7 +686,8 @@ def cpu_baseline(runs_1core: int = 3, runs_all: int = 5, quick: bool = False):
             secs.append(sec)
         st = _stats(secs)
         rows[f"config1_{name}"] = {
-            "threads": min(th, HEADS),  # one task per KV head "seconds": st, "us_per_layer_step": st["median"] / steps * 1e6,
+            "threads": min(th, HEADS),  # one task per KV head
+            "seconds": st, "us_per_layer_step": st["median"] / steps * 1e6,
             "GBs": c1_bytes / st["median"] / 1e9}
     del q, k, v
 
@@ -809,7 +811,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-widened", action="store_true")
     ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill",
-                                       "widened", "oproj"],
+                                       "widened", "oproj", "batch64", "long", "config1", "cpu"],
                     default=None,
                     help="profiling helper: run one leg only")
     args = ap.parse_args()
@@ -817,6 +819,9 @@ def main():
         print(f"bench.py measures one GPU: the KV-cache path runs on a single MI355X and "
               f"has no multi-GPU leg (asked for --gpus {args.gpus}).", file=sys.stderr)
         sys.exit(2)
+    if args.only == "cpu":
+        print(json.dumps(cpu_baseline(quick=args.cpu_quick)))
+        return
 
     import torch
     import gemma_kv as gk
@@ -839,6 +844,15 @@ def main():
         return
     if args.only == "widened":
         print(json.dumps(bench_widened(torch, gk, dev)))
+        return
+    if args.only == "batch64":
+        print(json.dumps(bench_batch64(torch, gk, dev, args.steps, args.warmup)))
+        return
+    if args.only == "long":
+        print(json.dumps(bench_long(torch, gk, dev, args.steps, args.warmup)))
+        return
+    if args.only == "config1":
+        print(json.dumps(bench_config1(torch, gk, dev)))
         return
     if args.only == "oproj":
         gen = torch.Generator(device=dev)

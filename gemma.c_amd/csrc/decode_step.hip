@@ -226,7 +226,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   __shared__ uint4 s_q[kWave];    // q rows of the unit: [g][pack]
   __shared__ uint4 s_new[kWave];  // appended rows of the unit: [K pack | V pack]
   __shared__ int32_t s_ticket;
-  __shared__ int32_t s_failed;
+  __shared__ int32_t s_failed, s_epoch, s_stall_layer, s_stall_ticks;
   __shared__ int4 s_lds_rows[kLdsSlots * kTileKeys / 4];  // cache rows of the LDS tiles
   extern __shared__ uint4 s_tiles[];  // [slot][K 0..3 | V 0..3][lane]
 
@@ -243,12 +243,17 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     s_ticket = (int32_t)(__hip_atomic_fetch_add(p.tickets + xcd * kTicketStride, 1u,
                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) %
                          kXcdSlots);
-    // A failed earlier launch (error recorded under another epoch) turns
-    // this launch into a no-op that writes zeros.
-    const int32_t err = coherent_load_i32(p.header + kHeaderError);
-    const int32_t err_epoch = coherent_load_i32(p.header + kHeaderErrorEpoch);
-    const int32_t ep = coherent_load_i32(p.header + kHeaderEpoch) + 1;
-    s_failed = err != 0 && err_epoch != ep;
+    // Header words 0..7 in one device-coherent load. A failed earlier
+    // launch (error recorded under another epoch) turns this launch into a
+    // no-op that writes zeros.
+    const BufferRsrc hdr = buffer_of(p.header, 32);
+    const u32x4 h0 = __builtin_amdgcn_raw_buffer_load_b128(hdr, 0, 0, kCoherentAux);
+    const u32x4 h1 = __builtin_amdgcn_raw_buffer_load_b128(hdr, 16, 0, kCoherentAux);
+    const int32_t ep = (int32_t)h0[kHeaderEpoch] + 1;
+    s_epoch = ep;
+    s_failed = h0[kHeaderError] != 0 && (int32_t)h0[kHeaderErrorEpoch] != ep;
+    s_stall_layer = (int32_t)h0[kHeaderStallLayer] - 1;
+    s_stall_ticks = (int32_t)h1[kHeaderStallTicks - 4];
   }
   __syncthreads();
   const int32_t ticket = wave_uniform(s_ticket);
@@ -266,7 +271,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   auto record = [&](int32_t s) -> int32_t {  // byte offset of split s's record
     return (u * p.splits + s) * (kRecordFloats * 4);
   };
-  const int32_t epoch = coherent_load_i32(p.header + kHeaderEpoch) + 1;
+  const int32_t epoch = wave_uniform(s_epoch);
   auto is_global_i = [&](int32_t i) { return model_layer_global(p.first_layer + i); };
   // Zeros for the output chunks this workgroup owns (those it combines:
   // c = split, split + splits, ... of both rows of unit u), layers from..end.
@@ -396,8 +401,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     }
     // Fault injection for tests: at layer stall_layer - 1, ticket 0 of XCD 0
     // waits, with the given limit, for a header word the host never sets.
-    const int32_t stall_layer = coherent_load_i32(p.header + kHeaderStallLayer) - 1;
-    const uint64_t stall_ticks = (uint32_t)coherent_load_i32(p.header + kHeaderStallTicks);
+    const int32_t stall_layer = wave_uniform(s_stall_layer);
+    const uint64_t stall_ticks = (uint32_t)wave_uniform(s_stall_ticks);
     // Layer `layer_i` is complete once all 8 XCD flags read `epoch`.
     auto wait_layer_device = [&](int32_t layer_i) {
       const int32_t *row = p.global_flags + layer_i * kGlobalFlagStride;
@@ -569,12 +574,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       wait_layer(p.layer_count - 1);
       if (lane == 0) coherent_store_i32(p.header + kHeaderEpoch, epoch);
     }
-    // Another workgroup's wait gave up during this launch: zero the chunks
-    // this one wrote as well (best effort: it sees the error only if it was
-    // recorded before this point; the status word is the contract).
-    if (coherent_load_i32(p.header + kHeaderError) != 0 &&
-        coherent_load_i32(p.header + kHeaderErrorEpoch) == epoch)
-      zero_own_chunks(0);
+    // This wave gave up a wait: its chunks of the layers before that are
+    // zeroed too, so none of its output is left from a failed step.
+    if (abort) zero_own_chunks(0);
     return;
   }
 

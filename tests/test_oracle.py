@@ -116,37 +116,53 @@ def test_invalid_row_write_known_answer():
     assert not ck.any() and not cv.any()
 
 
-def test_write_round_trip_and_skip_rules_brute_force():
+def test_write_skip_rules_and_gather_round_trip():
+    """Append semantics through invariants a wrong rule would fail, rather than
+    a restatement of the rules (src/gemma4_kv_cache.cu:25-54):
+    * a skipped row -- negative batch or position, batch past the config,
+      unmapped slot, physical page out of range, a global position past
+      max_pages_per_seq -- leaves a random cache byte-identical;
+    * a written row is found again by the attention's own page-table gather
+      (oracle_decode_attention over a window of one live key returns exactly
+      that V row for any q), for global and for wrapped sliding positions;
+    * a write changes exactly heads x head_dim elements of K and of V."""
     rng = np.random.default_rng(2)
-    page, max_pages, batch, heads, dim = 4, 3, 2, 2, 8
-    cfg = (2, batch * max_pages, page, max_pages, batch, heads, dim, 0)
-    pt = np.array([0, 1, -1, 3, 9, 5], np.int32)  # slot 2 unmapped, slot 4 out of range
-    tokens = 40
-    tb = rng.integers(-1, 3, tokens).astype(np.int32)
-    tp = rng.integers(-1, 14, tokens).astype(np.int32)
-    k = rng.integers(0, 1 << 16, (tokens, heads, dim)).astype(np.uint16)
-    v = rng.integers(0, 1 << 16, (tokens, heads, dim)).astype(np.uint16)
-    size = 2 * batch * max_pages * page * heads * dim
-    ck = np.zeros(size, np.uint16)
-    cv = np.zeros(size, np.uint16)
-    oracle.kv_cache_write(ck, cv, cfg, pt, tb, tp, 1, k, v)
-    exp_k = np.zeros(size, np.uint16)
-    exp_v = np.zeros(size, np.uint16)
-    for t in range(tokens):
-        b, p = tb[t], tp[t]
-        if b < 0 or p < 0 or b >= batch:
-            continue
-        lp = p // page
-        if lp >= max_pages:          # global cache: no wrap
-            continue
-        phys = pt[b * max_pages + lp]
-        if phys < 0 or phys >= batch * max_pages:
-            continue
-        for h in range(heads):
-            base = ((((1 * batch * max_pages + phys) * page + p % page) * heads) + h) * dim
-            exp_k[base:base + dim] = k[t, h]
-            exp_v[base:base + dim] = v[t, h]
-    assert np.array_equal(ck, exp_k) and np.array_equal(cv, exp_v)
+    page, max_pages, batch, heads, dim, layers = 4, 3, 2, 2, 8, 2
+    num_pages = batch * max_pages
+    pt = np.array([0, 1, -1, 3, 9, 5], np.int32)  # b0 slot 2 unmapped, b1 slot 1 -> page 9 (out of range)
+    size = layers * num_pages * page * heads * dim
+    base_k = rng.integers(0, 1 << 16, size).astype(np.uint16)
+    base_v = rng.integers(0, 1 << 16, size).astype(np.uint16)
+    glob = (layers, num_pages, page, max_pages, batch, heads, dim, 0)
+    slide = (layers, num_pages, page, max_pages, batch, heads, dim, 1)  # one live key
+
+    def write(cfg, b, p):
+        k = rng.integers(0, 1 << 15, (1, heads, dim)).astype(np.uint16)
+        v = rng.integers(0, 1 << 15, (1, heads, dim)).astype(np.uint16)
+        ck, cv = base_k.copy(), base_v.copy()
+        oracle.kv_cache_write(ck, cv, cfg, pt, [b], [p], 1, k, v)
+        return ck, cv, k, v
+
+    skipped = [(glob, -1, 0), (glob, 0, -1), (glob, 2, 0), (glob, 0, 8), (glob, 0, 9),
+               (glob, 1, 4), (glob, 0, 12), (glob, 1, 13), (slide, 0, 21), (slide, 1, 17)]
+    for cfg, b, p in skipped:
+        ck, cv, _, _ = write(cfg, b, p)
+        assert np.array_equal(ck, base_k) and np.array_equal(cv, base_v), (cfg[7], b, p)
+
+    written = [(glob, 0, 0), (glob, 0, 7), (glob, 1, 2), (glob, 1, 11),
+               (slide, 0, 12), (slide, 0, 19), (slide, 1, 14), (slide, 1, 23)]
+    for cfg, b, p in written:
+        ck, cv, k, v = write(cfg, b, p)
+        assert (ck != base_k).sum() <= heads * dim and (cv != base_v).sum() <= heads * dim
+        assert (ck != base_k).sum() > heads * dim // 2  # random rows: almost all differ
+        q = oracle.f32_to_bf16(rng.standard_normal((batch, 16, dim)).astype(np.float32))
+        one = (layers, num_pages, page, max_pages, batch, heads, dim, 1)
+        seq = np.zeros(batch, np.int32)
+        seq[b] = p + 1
+        out = oracle.decode_attention(q, ck, cv, pt, seq, one, 1, 0.125)
+        group = 16 // heads
+        for qh in range(16):
+            assert np.array_equal(out[b, qh], v[0, qh // group]), (cfg[7], b, p, qh)
 
 
 # ---- attention against a float64 library routine and closed forms --------------
