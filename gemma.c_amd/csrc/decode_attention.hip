@@ -30,6 +30,16 @@
 
 #include <algorithm>
 #include <math.h>
+#include <mutex>
+
+// Scratch of the allocation-free entry point
+// (gemma4_flash_attention_append_decode_paged_bf16_noalloc): the split
+// partials m, l, acc of one call, carved from this file-scope array. Each GPU
+// the library runs on holds its own copy (40 MiB) until the process ends;
+// host code reaches it only through the per-device address that
+// hipGetSymbolAddress returns (noalloc_scratch below).
+constexpr size_t kNoAllocScratchBytes = size_t(40) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 namespace gemma4 {
 namespace {
@@ -813,6 +823,29 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
   return hipErrorInvalidValue;
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch[kMaxDevices];  // per device: device address of `scratch`
+
+// Device address of the current device's `scratch`, looked up once per
+// device with that device current.
+hipError_t noalloc_scratch(float **out) {
+  int device = 0;
+  hipError_t e = hipGetDevice(&device);
+  if (e != hipSuccess) return e;
+  if (device < 0 || device >= kMaxDevices) return hipErrorNotSupported;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[device] == nullptr) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (ptr == nullptr) return hipErrorInvalidSymbol;
+    g_scratch[device] = static_cast<float *>(ptr);
+  }
+  *out = g_scratch[device];
+  return hipSuccess;
+}
+
 }  // namespace
 }  // namespace gemma4
 
@@ -855,6 +888,37 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
       d_token_position, reinterpret_cast<const uint16_t *>(d_k),
       reinterpret_cast<const uint16_t *>(d_v), d_split_counters, config, layer,
       softmax_scale,
+      split_size, num_splits, batch_count, /*combine=*/true, stream);
+}
+
+hipError_t gemma4_flash_attention_append_decode_paged_bf16_noalloc(
+    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table, const int32_t *d_seq_lengths,
+    const int32_t *d_token_position, const gemma4_bf16 *d_k, const gemma4_bf16 *d_v,
+    Gemma4KvCacheConfig config, int32_t layer, float softmax_scale, int32_t split_size,
+    int32_t num_splits, int32_t batch_count, hipStream_t stream) {
+  if (batch_count == 0) return hipSuccess;
+  if (d_token_position == nullptr || d_k == nullptr || d_v == nullptr || batch_count < 0 ||
+      num_splits <= 0 || (config.head_dim != 256 && config.head_dim != 512)) {
+    return hipErrorInvalidValue;
+  }
+  // Partials of this call: m and l [rows * splits], acc [rows * splits * D].
+  const int64_t slots = (int64_t)batch_count * kQueryHeads * num_splits;
+  const int64_t floats = slots * (2 + (int64_t)config.head_dim);
+  if (floats * (int64_t)sizeof(float) > (int64_t)kNoAllocScratchBytes) {
+    return hipErrorOutOfMemory;  // beyond the fixed scratch: use the workspace form
+  }
+  float *s = nullptr;
+  const hipError_t e = noalloc_scratch(&s);
+  if (e != hipSuccess) return e;
+  // The separate combine kernel reads only the live splits this call writes,
+  // so the scratch needs no clearing between calls.
+  return decode_entry(
+      reinterpret_cast<uint16_t *>(d_out), s, s + slots, s + 2 * slots,
+      reinterpret_cast<const uint16_t *>(d_q), reinterpret_cast<uint16_t *>(d_cache_k),
+      reinterpret_cast<uint16_t *>(d_cache_v), d_page_table, d_seq_lengths,
+      d_token_position, reinterpret_cast<const uint16_t *>(d_k),
+      reinterpret_cast<const uint16_t *>(d_v), nullptr, config, layer, softmax_scale,
       split_size, num_splits, batch_count, /*combine=*/true, stream);
 }
 

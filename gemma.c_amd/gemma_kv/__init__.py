@@ -107,6 +107,8 @@ SIGNATURES = {
     "gemma4_decode_step_workspace_init": (_I32, [_P, ctypes.c_size_t, _I32, _P]),
     "gemma4_decode_step_status": (_I32, [_P, ctypes.POINTER(_I32)]),
     "gemma4_decode_step_status_async": (_I32, [_P, _P, _P]),
+    "gemma4_flash_attention_append_decode_paged_bf16_noalloc": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_decode_step_inject_stall": (_I32, [_P, _I32, ctypes.c_uint32, _P]),
     "gemma4_decode_step_layers_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _CFG, _P, _P, _P, _CFG, _P, _P, _I32, _I32, _F32,
@@ -241,6 +243,17 @@ def flash_attention_append_decode_paged_bf16(out, partial_m, partial_l, partial_
         ptr(token_position), ptr(k), ptr(v), ptr(split_counters), config, layer,
         softmax_scale,
         split_size, num_splits, batch_count, stream_handle(stream))
+
+
+def flash_attention_append_decode_paged_bf16_noalloc(out, q, cache_k, cache_v, page_table,
+                                                     seq_lengths, token_position, k, v, config,
+                                                     layer, softmax_scale, split_size,
+                                                     num_splits, batch_count,
+                                                     stream=None) -> int:
+    return lib().gemma4_flash_attention_append_decode_paged_bf16_noalloc(
+        ptr(out), ptr(q), ptr(cache_k), ptr(cache_v), ptr(page_table), ptr(seq_lengths),
+        ptr(token_position), ptr(k), ptr(v), config, layer, softmax_scale, split_size,
+        num_splits, batch_count, stream_handle(stream))
 
 
 def flash_attention_decode_split_paged_bf16(out, partial_m, partial_l, partial_acc, q,

@@ -67,6 +67,24 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16(
     int32_t split_size, int32_t num_splits, int32_t batch_count,
     hipStream_t stream);
 
+// Allocation-free form of gemma4_flash_attention_append_decode_paged_bf16
+// (no counterpart in the reference): for callers that cannot allocate device
+// memory (code under HIP graph capture, tight serving loops, harnesses that
+// forbid hipMalloc). Same arguments without the partial buffers and split
+// counters; the split partials live in a fixed 40 MiB device array inside
+// the library (one per GPU, held until the process ends), the combine is the
+// separate kernel. Calls whose partials exceed it --
+// batch_count * 16 * num_splits * (head_dim + 2) * 4 bytes > 40 MiB -- return
+// hipErrorOutOfMemory before any launch. The call allocates nothing. All
+// calls on one GPU share that array: calls that overlap in time on one GPU
+// (different streams, or host threads) race and must not be issued.
+hipError_t gemma4_flash_attention_append_decode_paged_bf16_noalloc(
+    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, gemma4_bf16 *d_cache_k,
+    gemma4_bf16 *d_cache_v, const int32_t *d_page_table, const int32_t *d_seq_lengths,
+    const int32_t *d_token_position, const gemma4_bf16 *d_k, const gemma4_bf16 *d_v,
+    Gemma4KvCacheConfig config, int32_t layer, float softmax_scale, int32_t split_size,
+    int32_t num_splits, int32_t batch_count, hipStream_t stream);
+
 // Fused decode layer attention for raw projections: prepares q (learned
 // RMSNorm + RoPE at d_token_position[b]) inside every split workgroup, has the
 // split that owns the new key prepare its K (RMSNorm + RoPE) and V
