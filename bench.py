@@ -230,6 +230,53 @@ class StepRunner:
         return self.gk.decode_step_status(self.ws)
 
 
+def bench_step_ref_geometry(torch, gk, dev, layers, caches, meta, steps):
+    """Config 2 with the reference model's global geometry (1 KV head x 512,
+    src/gemma4.h:17-21) in place of 8 x 256: the same 40 sliding layers, 8
+    global layers over 8193 keys at 1 x 512. The step entry point runs the
+    sliding runs as persistent launches and each global layer as one fused
+    append + split-K launch (16 launches per step)."""
+    seq_len = CONTEXT + 1
+    g_pages = (seq_len + GLOBAL_PAGE - 1) // GLOBAL_PAGE
+    g_cfg = gk.make_config(8, g_pages, GLOBAL_PAGE, g_pages, 1, 1, 512, 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+
+    def rnd(shape):
+        return torch.randn(shape, generator=gen, device=dev).bfloat16().view(torch.int16)
+
+    gk_c, gv_c = rnd((8 * g_pages * GLOBAL_PAGE, 1, 512)), rnd((8 * g_pages * GLOBAL_PAGE, 1, 512))
+    qs, ks, vs, total = [], [], [], 0
+    for l in range(NUM_LAYERS):
+        h, d = (1, 512) if is_global_layer(l) else (HEADS, DIM)
+        qs.append(rnd((QH * d,)))
+        ks.append(rnd((h * d,)))
+        vs.append(rnd((h * d,)))
+        live = seq_len if is_global_layer(l) else WINDOW
+        total += live * 2 * h * d * 2 + 2 * h * d * 2 + 2 * QH * d * 2
+    q, k, v = torch.cat(qs), torch.cat(ks), torch.cat(vs)
+    out = torch.zeros_like(q)
+    s_cfg = next(L.cfg for L in layers if not L.is_global)
+    ws = torch.empty(gk.decode_step_workspace_bytes(1) // 4, dtype=torch.int32, device=dev)
+    gk.check(gk.decode_step_workspace_init(ws, 1), "workspace_init")
+
+    def fn(st):
+        gk.check(gk.decode_step_layers_bf16(
+            out, q, k, v, caches["sk"], caches["sv"], meta["s_pt"], s_cfg, gk_c, gv_c,
+            meta["g_pt"], g_cfg, meta["seq"], meta["pos"], 0, NUM_LAYERS, 1.0 / math.sqrt(DIM),
+            1, ws, stream=st), "decode_step 1x512")
+
+    warm_clock(torch, fn, 0.2)
+    ms = time_eager(torch, fn, steps, 3)
+    assert gk.decode_step_status(ws) == 0
+    del gk_c, gv_c
+    return {"workload": "config2 with 1x512 global layers (the reference model's geometry)",
+            "ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / NUM_LAYERS, 3),
+            "achieved_GBs": round(total / (ms * 1e-3) / 1e9, 1), "bytes_per_step": total,
+            "timing": "eager back-to-back steps: 8 persistent sliding runs + 8 fused "
+                      "global launches per step"}
+
+
 def bench_prefill(torch, gk, dev, reps):
     """a 2048-row prefill chunk on one sliding layer (window
     1024, 1024-slot page-1 ring after a 1536-token prior) and one global layer
@@ -811,7 +858,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-widened", action="store_true")
     ap.add_argument("--only", choices=["step", "persistent", "global", "copy", "prefill",
-                                       "widened", "oproj", "batch64", "long", "config1", "cpu"],
+                                       "widened", "oproj", "batch64", "long", "config1", "cpu",
+                                       "refgeo"],
                     default=None,
                     help="profiling helper: run one leg only")
     args = ap.parse_args()
@@ -864,6 +912,10 @@ def main():
     layers, caches, meta, scratch = build_config2(torch, gk, dev)
     step_bytes = sum(L.bytes for L in layers)
     runner = StepRunner(torch, gk, dev, layers, caches, meta)
+    if args.only == "refgeo":
+        print(json.dumps(bench_step_ref_geometry(torch, gk, dev, layers, caches, meta,
+                                                 args.steps)))
+        return
     if args.only == "persistent":
         for _ in range(args.steps):
             runner(torch.cuda.current_stream().cuda_stream)
@@ -968,6 +1020,8 @@ def main():
                                  "split_size": s_layers[0].split, "num_splits": s_layers[0].n_splits},
     }
     result["config1_gpu"] = bench_config1(torch, gk, dev)
+    result["step_reference_global_geometry"] = bench_step_ref_geometry(
+        torch, gk, dev, layers, caches, meta, max(10, args.steps // 2))
     if not args.no_batch64:
         b64 = bench_batch64(torch, gk, dev, max(3, args.steps // 5), 2)
         result["batch64"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in b64.items()}

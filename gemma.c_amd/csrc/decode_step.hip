@@ -903,11 +903,24 @@ __global__ void decode_step_workspace_init_kernel(int32_t *ints, int64_t n_ints,
     records[x] = kSentinel;
 }
 
+// The reference model's global geometry (1 KV head x 512, src/gemma4.h:17-21)
+// runs its layers as per-layer fused launches between the persistent runs,
+// with the separate combine kernel (the in-kernel combine would put all 16
+// query heads of a split set on one workgroup: 1.33 against 0.55 ms per
+// config-2 step); their split partials live in the workspace. Their split
+// plan targets one workgroup per CU (measured best against 128, 64 and 32),
+// so batch x splits <= 256 + batch.
+constexpr int kRefDim = 512;
+constexpr int kRefTargetWorkgroups = kStepWorkgroups;
+constexpr int64_t kRefPartialSlots = kRefTargetWorkgroups + kMaxBatch;  // (sequence, split) pairs
+
 // Workspace: header | XCD ticket counters | local flags | global flags |
-// probe slots | go flags | split records (sentinel-filled).
+// probe slots | go flags | split records (sentinel-filled) | 1x512 split
+// partials.
 struct WorkspaceLayout {
   int32_t units, splits;
-  int64_t tickets, local_flags, global_flags, probe, go_flags, int_count, record_floats, bytes;
+  int64_t tickets, local_flags, global_flags, probe, go_flags, int_count, record_floats,
+      ref_partial_floats, bytes;
 };
 WorkspaceLayout workspace_layout(int32_t batch_count) {
   WorkspaceLayout w{};
@@ -920,7 +933,8 @@ WorkspaceLayout workspace_layout(int32_t batch_count) {
   w.go_flags = w.probe + kStepWorkgroups;
   w.int_count = w.go_flags + (int64_t)kNumModelLayers * kXcds * 16;
   w.record_floats = (int64_t)w.units * w.splits * kRecordFloats;
-  w.bytes = (w.int_count + w.record_floats) * 4;
+  w.ref_partial_floats = kRefPartialSlots * kQueryHeads * (2 + kRefDim);
+  w.bytes = (w.int_count + w.record_floats + w.ref_partial_floats) * 4;
   return w;
 }
 
@@ -1052,6 +1066,55 @@ extern "C" hipError_t gemma4_decode_step_inject_stall(void *workspace, int32_t l
   return hipGetLastError();
 }
 
+namespace gemma4 {
+namespace {
+
+// One persistent launch over model layers [first_layer, first_layer + count),
+// all of them in 8 x 256 caches.
+hipError_t step_run(uint16_t *out, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                    gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
+                    const int32_t *const pt[2], const Gemma4KvCacheConfig cfg[2],
+                    const int32_t *seq_lengths, const int32_t *token_position,
+                    int32_t first_layer, int32_t layer_count, float scale,
+                    int32_t batch_count, void *workspace, hipStream_t stream) {
+  const WorkspaceLayout w = workspace_layout(batch_count);
+  bool need_kind[2] = {false, false};
+  for (int32_t l = first_layer; l < first_layer + layer_count; ++l)
+    need_kind[(l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0) ? 1 : 0] = true;
+  for (int kind = 0; kind < 2; ++kind) {
+    if (!need_kind[kind]) continue;
+    const Gemma4KvCacheConfig &c = cfg[kind];
+    if (ck[kind] == nullptr || cv[kind] == nullptr || pt[kind] == nullptr ||
+        !step_geometry_ok(c, batch_count) || (kind == 0) != (c.window_size > 0))
+      return hipErrorInvalidValue;
+    // Longest live key range a sequence can have in this cache, per split.
+    const int64_t live = kind == 0 ? c.window_size : (int64_t)c.max_pages_per_seq * c.page_size;
+    if ((live + w.splits - 1) / w.splits > kMaxSplitKeys) return hipErrorInvalidValue;
+    const int64_t rows = (int64_t)c.num_layers * c.num_pages * c.page_size;
+    if (rows * kRowElems >= (int64_t)1 << 31 || c.num_layers < 1) return hipErrorInvalidValue;
+  }
+  StepParams p = base_params(workspace, w, batch_count);
+  p.out = out;
+  p.q = q;
+  p.new_k = k;
+  p.new_v = v;
+  for (int kind = 0; kind < 2; ++kind) {
+    p.cache_k[kind] = reinterpret_cast<uint16_t *>(ck[kind]);
+    p.cache_v[kind] = reinterpret_cast<uint16_t *>(cv[kind]);
+    p.page_table[kind] = pt[kind];
+    p.c[kind] = cfg[kind];
+  }
+  p.seq_lengths = seq_lengths;
+  p.token_position = token_position;
+  p.first_layer = first_layer;
+  p.layer_count = layer_count;
+  p.q_scale = scale * kLog2e;
+  return launch_step(p, stream);
+}
+
+}  // namespace
+}  // namespace gemma4
+
 extern "C" hipError_t gemma4_decode_step_layers_bf16(
     gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
     gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
@@ -1067,45 +1130,80 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
       first_layer < 0 || layer_count < 1 || first_layer + layer_count > kNumModelLayers ||
       !(scale > 0.0f))
     return hipErrorInvalidValue;
-  const WorkspaceLayout w = workspace_layout(batch_count);
-  bool need_kind[2] = {false, false};
-  for (int32_t l = first_layer; l < first_layer + layer_count; ++l)
-    need_kind[(l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0) ? 1 : 0] = true;
-  const Gemma4KvCacheConfig cfg[2] = {sliding_config, global_config};
-  gemma4_bf16 *ck[2] = {sliding_cache_k, global_cache_k};
-  gemma4_bf16 *cv[2] = {sliding_cache_v, global_cache_v};
-  const int32_t *pt[2] = {sliding_page_table, global_page_table};
-  for (int kind = 0; kind < 2; ++kind) {
-    if (!need_kind[kind]) continue;
-    const Gemma4KvCacheConfig &c = cfg[kind];
-    if (ck[kind] == nullptr || cv[kind] == nullptr || pt[kind] == nullptr ||
-        !step_geometry_ok(c, batch_count) || (kind == 0) != (c.window_size > 0))
-      return hipErrorInvalidValue;
-    // Longest live key range a sequence can have in this cache, per split.
-    const int64_t live = kind == 0 ? c.window_size : (int64_t)c.max_pages_per_seq * c.page_size;
-    if ((live + w.splits - 1) / w.splits > kMaxSplitKeys) return hipErrorInvalidValue;
-    const int64_t rows = (int64_t)c.num_layers * c.num_pages * c.page_size;
-    if (rows * kRowElems >= (int64_t)1 << 31 || c.num_layers < 1) return hipErrorInvalidValue;
-  }
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64 ||
       g_placement_ok[device] != 1)
     return hipErrorNotSupported;  // gemma4_decode_step_workspace_init first
-  StepParams p = base_params(workspace, w, batch_count);
-  p.out = reinterpret_cast<uint16_t *>(out);
-  p.q = reinterpret_cast<const uint16_t *>(q);
-  p.new_k = reinterpret_cast<const uint16_t *>(k);
-  p.new_v = reinterpret_cast<const uint16_t *>(v);
-  for (int kind = 0; kind < 2; ++kind) {
-    p.cache_k[kind] = reinterpret_cast<uint16_t *>(ck[kind]);
-    p.cache_v[kind] = reinterpret_cast<uint16_t *>(cv[kind]);
-    p.page_table[kind] = pt[kind];
-    p.c[kind] = cfg[kind];
+  gemma4_bf16 *const ck[2] = {sliding_cache_k, global_cache_k};
+  gemma4_bf16 *const cv[2] = {sliding_cache_v, global_cache_v};
+  const int32_t *const pt[2] = {sliding_page_table, global_page_table};
+  const Gemma4KvCacheConfig cfg[2] = {sliding_config, global_config};
+  const bool ref_global = global_config.num_heads == 1 && global_config.head_dim == kRefDim;
+  auto is_global = [](int32_t l) { return l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0; };
+  const int32_t last = first_layer + layer_count;
+  if (!ref_global) {
+    return step_run(reinterpret_cast<uint16_t *>(out), reinterpret_cast<const uint16_t *>(q),
+                    reinterpret_cast<const uint16_t *>(k), reinterpret_cast<const uint16_t *>(v),
+                    ck, cv, pt, cfg, seq_lengths, token_position, first_layer, layer_count,
+                    scale, batch_count, workspace, stream);
   }
-  p.seq_lengths = seq_lengths;
-  p.token_position = token_position;
-  p.first_layer = first_layer;
-  p.layer_count = layer_count;
-  p.q_scale = scale * kLog2e;
-  return launch_step(p, stream);
+  // Reference global geometry: runs of sliding layers go to the persistent
+  // kernel, each global layer to one fused append + split-K launch with the
+  // in-kernel combine (its partials and counters in the workspace). Stream
+  // order keeps layer i after layer i-1. Rows are laid out back to back,
+  // layer by layer, each layer's [batch][16][head_dim] (q, out) and
+  // [batch][Hk][head_dim] (k, v) at its own width.
+  int32_t ref_split = 0, ref_splits = 0;
+  bool have_global = false;
+  for (int32_t l = first_layer; l < last; ++l) have_global |= is_global(l);
+  if (have_global) {
+    const Gemma4KvCacheConfig &g = global_config;
+    if (g.window_size != 0 || g.batch_size < batch_count || g.max_pages_per_seq <= 0 ||
+        g.page_size <= 0)
+      return hipErrorInvalidValue;
+    const int64_t capacity = (int64_t)g.max_pages_per_seq * g.page_size;
+    if (capacity > 0x7fffffff) return hipErrorInvalidValue;
+    const hipError_t e = gemma4_decode_split_plan(g, batch_count, (int32_t)capacity,
+                                                  kRefTargetWorkgroups, &ref_split, &ref_splits);
+    if (e != hipSuccess) return e;
+    if ((int64_t)batch_count * ref_splits > kRefPartialSlots) return hipErrorInvalidValue;
+  }
+  const WorkspaceLayout w = workspace_layout(batch_count);
+  int32_t *ints = static_cast<int32_t *>(workspace);
+  float *ref_partials = reinterpret_cast<float *>(ints + w.int_count) + w.record_floats;
+  const int64_t rows = (int64_t)batch_count * kQueryHeads;
+  const uint16_t *qp = reinterpret_cast<const uint16_t *>(q);
+  const uint16_t *kp = reinterpret_cast<const uint16_t *>(k);
+  const uint16_t *vp = reinterpret_cast<const uint16_t *>(v);
+  uint16_t *op = reinterpret_cast<uint16_t *>(out);
+  for (int32_t l = first_layer; l < last;) {
+    if (is_global(l)) {
+      const int64_t slots = rows * ref_splits;
+      const hipError_t e = gemma4_flash_attention_append_decode_paged_bf16(
+          reinterpret_cast<gemma4_bf16 *>(op), ref_partials, ref_partials + slots,
+          ref_partials + 2 * slots, reinterpret_cast<const gemma4_bf16 *>(qp),
+          global_cache_k, global_cache_v, global_page_table, seq_lengths, token_position,
+          reinterpret_cast<const gemma4_bf16 *>(kp), reinterpret_cast<const gemma4_bf16 *>(vp),
+          nullptr, global_config, gemma4_kv_cache_layer_index(l, true), scale,
+          ref_split, ref_splits, batch_count, stream);
+      if (e != hipSuccess) return e;
+      qp += rows * kRefDim;
+      op += rows * kRefDim;
+      kp += (int64_t)batch_count * kRefDim;
+      vp += (int64_t)batch_count * kRefDim;
+      ++l;
+      continue;
+    }
+    int32_t run = 0;
+    while (l + run < last && !is_global(l + run)) ++run;
+    const hipError_t e = step_run(op, qp, kp, vp, ck, cv, pt, cfg, seq_lengths, token_position,
+                                  l, run, scale, batch_count, workspace, stream);
+    if (e != hipSuccess) return e;
+    qp += run * rows * kSDim;
+    op += run * rows * kSDim;
+    kp += (int64_t)run * batch_count * kRowElems;
+    vp += (int64_t)run * batch_count * kRowElems;
+    l += run;
+  }
+  return hipSuccess;
 }

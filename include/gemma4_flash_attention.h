@@ -221,13 +221,19 @@ hipError_t gemma4_decode_prep_append_bf16(
 // launches of the reference decode loop (src/gemma4_decode_megakernel.cu:172-183
 // -> gemma4_decode_megakernel_flash_attention_layer_bf16, append + attention
 // phases src/gemma4_flash_attention_decode.cu:979-1067).
-//   q, out: [layer_count][batch_count][16][256] bf16; k, v (the appended
-//   rows): [layer_count][batch_count][8][256]. Layer i reads q/k/v[i] only
-//   after out[i-1] is complete (the order a real decode step imposes).
 //   Sliding layers use the sliding cache/config/page table, global layers
-//   (every 6th and the last) the global ones; both geometries must be 8 KV
-//   heads x 256 (the reference model's 1 x 512 global geometry is served by
-//   the per-layer entry points). seq_lengths / token_position: as for the
+//   (every 6th and the last) the global ones. Sliding geometry: 8 KV heads
+//   x 256. Global geometry: 8 x 256 (all layers then run in the persistent
+//   launch), or the reference model's 1 KV head x 512 (src/gemma4.h:17-21):
+//   then each run of sliding layers is one persistent launch and each global
+//   layer one fused append + split-K launch with its combine, all in stream
+//   order (16 launches for 48 layers).
+//   q, out / k, v (the appended rows): the layers' rows back to back, layer
+//   by layer, each layer's [batch_count][16][head_dim] (q, out) and
+//   [batch_count][num_heads][head_dim] (k, v) at its own geometry; with 8 x
+//   256 everywhere that is [layer_count][batch_count][16 or 8][256]. Layer i
+//   reads its q/k/v only after layer i-1's output is complete (the order a
+//   real decode step imposes). seq_lengths / token_position: as for the
 //   per-layer entry points (one step: the same for every layer).
 // `workspace` (gemma4_decode_step_workspace_bytes bytes) holds the split
 // records and layer flags; initialise it once with
@@ -235,6 +241,8 @@ hipError_t gemma4_decode_prep_append_bf16(
 // that the workgroups land one per CU, 32 per XCD; hipErrorNotSupported
 // otherwise), then reuse it for every step (stream order). Calls sharing a
 // workspace must not overlap.
+// With the 1 x 512 global geometry the global layers' launches are not gated
+// by the status below (only the persistent launches are).
 // Failure is stream-ordered and sticky: every wait of the step is bounded
 // (0.2 s); if one gives up (another kernel held CUs), the launch writes
 // zeros for the output chunks whose wait gave up and records a nonzero

@@ -121,6 +121,82 @@ def test_decode_step_against_oracle(dev, first, count, seq, window, s_page, g_pa
     assert np.array_equal(again, got)
 
 
+REF_CASES = [
+    # first_layer, layer_count, seq_lengths, window, sliding page, global page
+    (0, 7, [151], 64, 1, 16),             # sliding run, 1x512 global layer 5, sliding 6
+    (44, 4, [300, 77], 128, 1, 64),       # batch 2, ends at the last (global) layer
+    (5, 1, [1], 1024, 1, 64),             # one global layer, first token
+    (3, 9, [40, 9, 513], 256, 16, 16),    # batch 3, globals 5 and 11, ragged
+]
+
+
+@pytest.mark.parametrize("first,count,seq,window,s_page,g_page", REF_CASES)
+def test_decode_step_reference_global_geometry(dev, first, count, seq, window, s_page, g_page):
+    """The reference model's own geometry (src/gemma4.h:17-21): sliding layers
+    8 x 256, global layers 1 KV head x 512 (GQA 16). Rows of q/k/v/out are laid
+    out layer by layer at each layer's width. Checked against the oracle
+    applied layer by layer: caches bit-exact, outputs within tolerance; a
+    second step on the same workspace gives the same outputs."""
+    import torch
+    rng = np.random.default_rng(sum(seq) * 3 + first + count)
+    batch = len(seq)
+    layers = list(range(first, first + count))
+    n_s = sum(1 for l in range(48) if not is_global(l))
+    n_g = 48 - n_s
+    s_max = ring_pages(window, s_page)
+    g_max = (max(seq) + g_page - 1) // g_page
+    s_cfg = cache_config(n_s, batch, s_page, s_max, HEADS, DIM, window)
+    g_cfg = cache_config(n_g, batch, g_page, g_max, 1, 512, 0)
+    s_pt = fill_page_table(s_cfg, seq)
+    g_pt = fill_page_table(g_cfg, seq)
+    caches = {
+        "sk": randn_bf16(rng, (s_cfg[0] * s_cfg[1] * s_page, HEADS, DIM)),
+        "sv": randn_bf16(rng, (s_cfg[0] * s_cfg[1] * s_page, HEADS, DIM)),
+        "gk": randn_bf16(rng, (g_cfg[0] * g_cfg[1] * g_page, 1, 512)),
+        "gv": randn_bf16(rng, (g_cfg[0] * g_cfg[1] * g_page, 1, 512)),
+    }
+    geo = [(1, 512) if is_global(l) else (HEADS, DIM) for l in layers]
+    qs = [randn_bf16(rng, (batch, 16, d)) for _, d in geo]
+    ks = [randn_bf16(rng, (batch, h, d)) for h, d in geo]
+    vs = [randn_bf16(rng, (batch, h, d)) for h, d in geo]
+    pos = [n - 1 for n in seq]
+    scale = 1 / math.sqrt(DIM)
+    exp = {n: a.copy() for n, a in caches.items()}
+    exp_out = []
+    for i, layer in enumerate(layers):
+        g = is_global(layer)
+        cfg, pt = (g_cfg, g_pt) if g else (s_cfg, s_pt)
+        ck, cv = (exp["gk"], exp["gv"]) if g else (exp["sk"], exp["sv"])
+        cl = oracle.layer_index(layer, g)
+        oracle.kv_cache_write(ck, cv, cfg, pt, list(range(batch)), pos, cl, ks[i], vs[i])
+        exp_out.append(oracle.decode_attention(qs[i], ck, cv, pt, seq, cfg, cl, scale))
+    flat = lambda arrs: np.concatenate([a.reshape(-1) for a in arrs])
+    d = {n: to_dev(a, dev) for n, a in caches.items()}
+    dq, dk, dv = to_dev(flat(qs), dev), to_dev(flat(ks), dev), to_dev(flat(vs), dev)
+    ws = _workspace(dev, batch)
+    outs = []
+    for rep in range(2):
+        out = torch.zeros(sum(batch * 16 * dd for _, dd in geo), dtype=torch.int16, device=dev)
+        gk.check(gk.decode_step_layers_bf16(
+            out, dq, dk, dv, d["sk"], d["sv"], to_dev(s_pt, dev), gk.make_config(*s_cfg),
+            d["gk"], d["gv"], to_dev(g_pt, dev), gk.make_config(*g_cfg),
+            to_dev(np.asarray(seq, np.int32), dev), to_dev(np.asarray(pos, np.int32), dev),
+            first, count, scale, batch, ws), "decode_step 1x512")
+        torch.cuda.synchronize()
+        assert gk.decode_step_status(ws) == 0
+        outs.append(from_dev_bf16(out))
+        if rep == 0:
+            for n in caches:
+                assert np.array_equal(from_dev_bf16(d[n]).reshape(caches[n].shape), exp[n]), n
+    assert np.array_equal(outs[0], outs[1])
+    off = 0
+    for i, layer in enumerate(layers):
+        size = batch * 16 * geo[i][1]
+        assert_close(outs[0][off:off + size].reshape(batch, 16, geo[i][1]), exp_out[i],
+                     f"layer {layer}")
+        off += size
+
+
 def test_decode_step_failure_is_reported_and_sticky(dev):
     """A bounded wait made to give up from the host (fault injection: at layer
     2 one workgroup waits for a word nothing sets, limit 20 us) while every
@@ -186,7 +262,7 @@ def test_decode_step_rejects_bad_arguments(dev):
     assert gk.decode_step_layers_bf16(*args, 0, 2, 0.0625, 9, ws) != 0    # batch > 8
     bad = list(args)
     bad[7] = bad_geom
-    assert gk.decode_step_layers_bf16(*bad, 0, 2, 0.0625, 1, ws) != 0     # 1x512
+    assert gk.decode_step_layers_bf16(*bad, 0, 2, 0.0625, 1, ws) != 0     # sliding 1x512
     small = torch.empty(16, dtype=torch.int32, device=dev)
     assert gk.decode_step_layers_bf16(*args, 0, 2, 0.0625, 1, small) != 0  # workspace
     torch.cuda.synchronize()
