@@ -24,12 +24,12 @@
 //   every sequence: sequence b = t % batch, split s = t / batch, with
 //   splits = 32 / batch per (sequence, head) "unit". All splits of a unit
 //   therefore share one L2, and their partials are exchanged through it.
-//   compute waves 0..3: 8-key tiles t = wave, wave+4, ... of the split
-//   control wave 4:     waits for the previous layer, stages the layer's q
+//   compute waves 0..7: 8-key tiles t = wave, wave+8, ... of the split
+//   control wave 8:     waits for the previous layer, stages the layer's q
 //                       and appended K/V rows in LDS, then combines the
 //                       unit's splits for its own 8-dim output chunks
 //                       (c = s, s + splits, ...) and signals
-//   prefetch wave 5:    DMAs the next global layer's tiles 16..32 of the
+//   prefetch wave 9:    DMAs the next global layer's tiles 16..31 of the
 //                       split into LDS (global_load_lds), a few per barrier
 //                       interval over the 4 layers before it
 // A tile is 8 keys x 256 dims of K and V: lane (r, c) loads the 16-byte pack
@@ -72,6 +72,7 @@
 
 #include <math.h>
 
+
 namespace gemma4 {
 namespace {
 
@@ -80,9 +81,12 @@ namespace {
 constexpr int32_t kNumModelLayers = 48;
 constexpr int32_t kGlobalPeriod = 6;
 constexpr int kSHeads = 8, kSDim = 256, kSGroup = 2;
-constexpr int kComputeWaves = 4;
-constexpr int kControlWave = kComputeWaves;      // wave 4
-constexpr int kPrefetchWave = kComputeWaves + 1; // wave 5
+// Eight compute waves, two per SIMD (163 VGPRs each, three waves on two of
+// the SIMDs with the control and prefetch waves): 382 against 392 us per
+// config-2 step with four, mostly from the global layers' tile compute.
+constexpr int kComputeWaves = 8;
+constexpr int kControlWave = kComputeWaves;      // wave 8
+constexpr int kPrefetchWave = kComputeWaves + 1; // wave 9
 constexpr int kStepThreads = (kComputeWaves + 2) * kWave;
 constexpr int kStepWorkgroups = 256;  // one workgroup per CU
 constexpr int kLPR = kSDim / kPackElems;      // 32 lanes per key row
@@ -114,12 +118,13 @@ constexpr int kHeaderStallLayer = 3, kHeaderStallTicks = 4, kHeaderNeverSet = 5;
 constexpr int kTicketStride = 32;             // ints between the XCD ticket counters
 constexpr int kGlobalFlagStride = 16;         // ints per layer: one flag per XCD
 constexpr uint64_t kWaitTicks = 100ull * 1000 * 1000 / 5;  // 0.2 s at 100 MHz
-constexpr int kPrefetchTiles = 4;             // register tile buffers per wave
+constexpr int kPrefetchTiles = 16 / kComputeWaves;  // register tile buffers per wave
 // Global-layer tiles staged in LDS ahead of time by the prefetch wave: the
-// wave's tiles 16.. of a split (after the 16 held in compute-wave
-// registers). 17 x 8 KiB = 136 KiB of dynamic LDS, which also keeps the
-// hardware to one workgroup per CU.
-constexpr int kLdsSlots = 17;
+// split's tiles 16..31 (after the 16 held in compute-wave registers, two
+// per wave). 16 x 8 KiB = 128 KiB of dynamic LDS (with the 29 KiB of static
+// arrays, all of a CU's 160 KiB), which also keeps the hardware to one
+// workgroup per CU.
+constexpr int kLdsSlots = 16;
 constexpr int kRegTiles = kComputeWaves * kPrefetchTiles;  // tiles 0..15 of a split: registers
 constexpr int kLdsLead = 4;                    // layers of lead for the LDS prefetch
 constexpr int kSlotsPerInterval = 2;           // slots requested between two barriers
@@ -143,6 +148,7 @@ struct StepParams {
   int32_t *go_flags;      // [layer][xcd][16]: XCD-local copy of "layer complete"
   float *records;
   int32_t *probe;         // non-null: only report each workgroup's XCD id
+  uint64_t *trace;        // STEP_TRACE builds: [workgroup][layer][10] real-time stamps
   int32_t batch;
   int32_t first_layer;
   int32_t layer_count;
@@ -162,7 +168,31 @@ __device__ __forceinline__ int32_t cache_layer_of(int32_t layer) {
   return index;
 }
 
+// Workgroup barrier of the step kernel. A barrier that waits only for LDS
+// traffic (leaving register-tile loads and LDS DMA in flight across it) was
+// measured no faster (392 against 382 us per config-2 step): the first use
+// of a register tile waits for it anyway.
+__device__ __forceinline__ void step_barrier() { __syncthreads(); }
+
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
+
+// Development builds only (-DSTEP_TRACE=1): real-time stamps of the layer
+// phases, [workgroup (xcd * 32 + ticket)][layer][10], in the workspace.
+#ifndef STEP_TRACE
+#define STEP_TRACE 0
+#endif
+#if STEP_TRACE
+#define STEP_MARK(e)                                                                     \
+  do {                                                                                   \
+    if (lane == 0 && (wave == kControlWave || wave == 0))                                \
+      p.trace[((int64_t)(xcd * kXcdSlots + ticket) * kNumModelLayers + i) * 10 + (e)] = \
+          now_ticks();                                                                   \
+  } while (0)
+#else
+#define STEP_MARK(e) \
+  do {               \
+  } while (0)
+#endif
 
 // Id of the XCD (and so of the L2) this wave runs on.
 __device__ __forceinline__ uint32_t xcc_id() {
@@ -255,7 +285,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     s_stall_layer = (int32_t)h0[kHeaderStallLayer] - 1;
     s_stall_ticks = (int32_t)h1[kHeaderStallTicks - 4];
   }
-  __syncthreads();
+  step_barrier();
   const int32_t ticket = wave_uniform(s_ticket);
   const bool active = ticket < p.batch * p.splits;
   const int32_t b = active ? ticket % p.batch : 0;
@@ -363,11 +393,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         request(kLdsSlots);
         wait_stores_complete();
       }
-      __syncthreads();  // A
+      step_barrier();  // A
       if (target > i) request(kSlotsPerInterval);
-      __syncthreads();  // B
+      step_barrier();  // B
       if (target > i) request(kSlotsPerInterval);
-      __syncthreads();  // C
+      step_barrier();  // C
       maybe_plan(i);
       if (target > i) request(kSlotsPerInterval);
     }
@@ -457,7 +487,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     const BufferRsrc in_buf_k = buffer_of(p.new_k, (int64_t)p.layer_count * kv_stride * 2);
     const BufferRsrc in_buf_v = buffer_of(p.new_v, (int64_t)p.layer_count * kv_stride * 2);
     for (int32_t i = 0; i < p.layer_count; ++i) {
+      STEP_MARK(0);
       if (i > 0) wait_layer(i - 1);
+      STEP_MARK(1);
       if (i == stall_layer && xcd == 0 && ticket == 0) {
         const uint64_t t0 = now_ticks();
         while (!abort && coherent_load_i32(p.header + kHeaderNeverSet) != epoch) {
@@ -477,8 +509,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         s_q[lane] = make_uint4(qv[0], qv[1], qv[2], qv[3]);
         s_new[lane] = make_uint4(nv[0], nv[1], nv[2], nv[3]);
       }
-      __syncthreads();  // A: layer i may start
-      __syncthreads();  // B: this workgroup's compute waves finished layer i
+      STEP_MARK(2);
+      step_barrier();  // A: layer i may start
+      step_barrier();  // B: this workgroup's compute waves finished layer i
+      STEP_MARK(5);
 
       // Combine unit u's splits for the 8-dim chunks c = split, split +
       // splits, ... of both rows: one round of L2 loads per chunk; the
@@ -560,7 +594,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
           __builtin_amdgcn_raw_buffer_store_b64(s2, rec_buf, off + 32, 0, 0);
         }
       }
-      __syncthreads();  // C: records read; compute waves may prefetch
+      STEP_MARK(6);
+      step_barrier();  // C: records read; compute waves may prefetch
       // My output slices and chunk resets are complete before my local flag.
       wait_stores_complete();
       if (lane == 0) {
@@ -568,6 +603,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
                                               ((i * kXcds + xcd) * kXcdSlots + ticket) * 4, 0, 0);
       }
       if (ticket == 0) publish_xcd(i);
+      STEP_MARK(7);
     }
     if (xcd == 0 && ticket == 0) {
       // Every workgroup has read the header (and finished): advance it.
@@ -711,22 +747,44 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       pv[i] = q4.x; pv[i + 1] = q4.y; pv[i + 2] = q4.z; pv[i + 3] = q4.w;
     }
   };
+  // P.V on v_dot2 over key pairs: the probabilities of keys (0, 1) and
+  // (2, 3) of the lane's row half are packed as bf16 pairs (RNE), and each V
+  // word pair of those keys is regrouped by dim with one byte permute, so a
+  // dot2 adds both keys' terms of one dim (fp32 products and sums).
   auto accumulate = [&](const uint4 (&v)[kTileLoads], uint32_t valid_bits) {
 #pragma unroll
     for (int g = 0; g < kSGroup; ++g) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[g][j] *= alpha[g];
     }
+    uint32_t w[kTileLoads][4];
 #pragma unroll
     for (int kl = 0; kl < kTileLoads; ++kl) {
-      float vf[8];
-      const uint4 vp = (valid_bits >> kl) & 1u ? v[kl] : make_uint4(0, 0, 0, 0);
-      unpack8(vp, vf);
+      const bool ok = (valid_bits >> kl) & 1u;
+      w[kl][0] = ok ? v[kl].x : 0u;
+      w[kl][1] = ok ? v[kl].y : 0u;
+      w[kl][2] = ok ? v[kl].z : 0u;
+      w[kl][3] = ok ? v[kl].w : 0u;
+    }
+#pragma unroll
+    for (int pr = 0; pr < kTileLoads / 2; ++pr) {
+      uint32_t pp[kSGroup];
 #pragma unroll
       for (int g = 0; g < kSGroup; ++g) {
-        const float w = pv[kl * kSGroup + g];
+        const bf16x2_t pair = {(__bf16)pv[(2 * pr) * kSGroup + g],
+                               (__bf16)pv[(2 * pr + 1) * kSGroup + g]};
+        pp[g] = __builtin_bit_cast(uint32_t, pair);
+      }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[g][j] = fmaf(w, vf[j], acc[g][j]);
+      for (int wi = 0; wi < 4; ++wi) {
+        const uint32_t a = w[2 * pr][wi], b = w[2 * pr + 1][wi];
+        const uint32_t lo = __builtin_amdgcn_perm(b, a, 0x05040100u);  // dim 2wi of both keys
+        const uint32_t hi = __builtin_amdgcn_perm(b, a, 0x07060302u);  // dim 2wi + 1
+#pragma unroll
+        for (int g = 0; g < kSGroup; ++g) {
+          acc[g][2 * wi] = dot2_bf16(pp[g], lo, acc[g][2 * wi]);
+          acc[g][2 * wi + 1] = dot2_bf16(pp[g], hi, acc[g][2 * wi + 1]);
+        }
       }
     }
   };
@@ -757,10 +815,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     }
   };
 
-  // Register prefetch: at the end of layer i (barrier C) the first four
-  // tiles of layer i+1 are issued. (Issuing a global layer's register tiles
-  // several layers ahead was measured slower: the waits of the layers in
-  // between then cover those loads too.)
+  // Register prefetch: at the end of layer i (barrier C) the first tiles of
+  // layer i+1 are requested. (Issuing them earlier -- several layers ahead
+  // for a global layer, or two layers ahead for sliding ones -- was measured
+  // slower: the waits of the layers in between then cover those loads too.)
   TileBuf buf[kPrefetchTiles];
   LayerView cur;
   auto prepare = [&](int32_t i) {  // at the end of layer i (i = -1: start)
@@ -775,13 +833,15 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
 
   // This wave's record dwords: head g = lane / 32, dims d, d+1 of its
   // quarter, inside 8-dim chunk d / 8 (whose first lane also writes m, l).
+  constexpr int kMergeDims = kSDim / kComputeWaves / kLPR;  // dims per lane
   const int rec_g = lane / kLPR;
-  const int rec_d = wave * (kSDim / kComputeWaves) + (lane % kLPR) * 2;
+  const int rec_d = wave * (kSDim / kComputeWaves) + (lane % kLPR) * kMergeDims;
   const int32_t rec_acc = (rec_d / kPackElems * kChunkFloats + rec_g * kHalfChunk + rec_d % kPackElems) * 4;
   const int32_t rec_ml = (rec_d / kPackElems * kChunkFloats + rec_g * kHalfChunk + kPackElems) * 4;
 
   for (int32_t i = 0; i < p.layer_count; ++i) {
-    __syncthreads();  // A: layer i-1 published (or i == 0), inputs in LDS
+    step_barrier();  // A: layer i-1 published (or i == 0), inputs in LDS
+    STEP_MARK(3);
     const LayerView view = cur;
 #pragma unroll
     for (int g = 0; g < kSGroup; ++g) {
@@ -845,7 +905,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       store128(p.cache_v[view.kind] + dst, s_new[kLPR + cpack]);
     }
 
-    // Wave totals to LDS, then the four waves' partials are merged.
+    // Wave totals to LDS, then the compute waves' partials are merged.
     float l_head[kSGroup];
     gather_heads<kSGroup, kSBits>(reduce_sum_from<(1 << kSBits) * kSGroup>(l_lane), my_g, l_head);
 #pragma unroll
@@ -868,7 +928,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
       }
     }
-    __syncthreads();  // B
+    STEP_MARK(4);
+    step_barrier();  // B
     if (active) {
       float big_m = -INFINITY;
 #pragma unroll
@@ -879,17 +940,27 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       for (int w = 0; w < kComputeWaves; ++w) {
         const float f = __builtin_amdgcn_exp2f(s_ml[w][rec_g][0] - m_ref);
         big_l = fmaf(s_ml[w][rec_g][1], f, big_l);
-        const float2 a = *reinterpret_cast<const float2 *>(&s_acc[w][rec_g][rec_d]);
-        a0 = fmaf(a.x, f, a0);
-        a1 = fmaf(a.y, f, a1);
+        if constexpr (kMergeDims == 2) {
+          const float2 a = *reinterpret_cast<const float2 *>(&s_acc[w][rec_g][rec_d]);
+          a0 = fmaf(a.x, f, a0);
+          a1 = fmaf(a.y, f, a1);
+        } else {
+          a0 = fmaf(s_acc[w][rec_g][rec_d], f, a0);
+        }
       }
       // The chunk was emptied by its reader before the previous layer
       // completed, so these stores need no wait.
       const int32_t rec = record(split);
-      local_store2(rec_buf, rec + rec_acc, a0, a1);
+      if constexpr (kMergeDims == 2) {
+        local_store2(rec_buf, rec + rec_acc, a0, a1);
+      } else {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(a0), rec_buf, rec + rec_acc, 0, 0);
+        (void)a1;
+      }
       if (rec_d % kPackElems == 0) local_store2(rec_buf, rec + rec_ml, big_m, big_l);
     }
-    __syncthreads();  // C: the control wave has read the split records
+    STEP_MARK(9);
+    step_barrier();  // C: the control wave has read the split records
     prepare(i);
   }
 }
@@ -935,6 +1006,8 @@ WorkspaceLayout workspace_layout(int32_t batch_count) {
   w.record_floats = (int64_t)w.units * w.splits * kRecordFloats;
   w.ref_partial_floats = kRefPartialSlots * kQueryHeads * (2 + kRefDim);
   w.bytes = (w.int_count + w.record_floats + w.ref_partial_floats) * 4;
+  w.bytes = (w.bytes + 7) / 8 * 8;
+  if (STEP_TRACE) w.bytes += (int64_t)kStepWorkgroups * kNumModelLayers * 10 * 8;
   return w;
 }
 
@@ -950,6 +1023,10 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
   p.global_flags = ints + w.global_flags;
   p.go_flags = ints + w.go_flags;
   p.records = reinterpret_cast<float *>(ints + w.int_count);
+  if (STEP_TRACE) {
+    const int64_t off = ((w.int_count + w.record_floats + w.ref_partial_floats) * 4 + 7) / 8 * 8;
+    p.trace = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + off);
+  }
   p.batch = batch_count;
   p.units = w.units;
   p.splits = w.splits;
