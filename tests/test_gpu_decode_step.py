@@ -93,6 +93,7 @@ STEP_CASES = [
     (44, 4, [300, 77], 128, 1, 64),    # batch 2, ends at the last (global) layer
     (5, 1, [1], 1024, 1, 64),          # one global layer, first token
     (0, 6, [2000, 1, 513], 256, 16, 64),  # batch 3 (10 splits per unit), ragged
+    (3, 9, [3000, 1, 513, 64, 1024, 2, 700, 9], 1024, 16, 64),  # batch 8: 4 splits per unit
 ]
 
 

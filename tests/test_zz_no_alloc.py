@@ -76,6 +76,35 @@ def test_noalloc_matches_workspace_form_on_two_calls(dev):
     assert 4 * n1 * 256 > n2 * 512  # the second call's partials are the smaller
 
 
+def test_noalloc_single_split_writes_directly(dev):
+    """num_splits == 1: no partials at all (the direct-output path), same
+    result as the workspace form."""
+    import torch
+    rng = np.random.default_rng(5)
+    seq = [40, 7]
+    cfg, pt, ck, cv, q, k, v = _case(rng, seq, 8, 256, 0, 16)
+    conf = gk.make_config(*cfg)
+    d_seq = to_dev(np.asarray(seq, np.int32), dev)
+    d_pos = to_dev(np.asarray([n - 1 for n in seq], np.int32), dev)
+    d_pt, d_q, d_k, d_v = to_dev(pt, dev), to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
+    outs = []
+    for noalloc in (False, True):
+        c_k, c_v = to_dev(ck, dev), to_dev(cv, dev)
+        out = torch.zeros((2, 16, 256), dtype=torch.int16, device=dev)
+        if noalloc:
+            code = gk.flash_attention_append_decode_paged_bf16_noalloc(
+                out, d_q, c_k, c_v, d_pt, d_seq, d_pos, d_k, d_v, conf, 0, 0.0625, 64, 1, 2)
+        else:
+            code = gk.flash_attention_append_decode_paged_bf16(
+                out, None, None, None, d_q, c_k, c_v, d_pt, d_seq, d_pos, d_k, d_v, conf, 0,
+                0.0625, 64, 1, 2)
+        gk.check(code, "single split")
+        torch.cuda.synchronize()
+        outs.append((out, c_k, c_v))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+
+
 def test_noalloc_rejects_calls_past_the_scratch(dev):
     import torch
     conf = gk.make_config(1, 64, 64, 1, 64, 8, 256, 0)
