@@ -72,6 +72,8 @@
 
 #include <math.h>
 
+#include <atomic>
+
 
 namespace gemma4 {
 namespace {
@@ -1033,17 +1035,27 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
   return p;
 }
 
-// Every launch of the step kernel, the placement probe at workspace
-// initialisation included, is an ordinary launch. The probe checks that the
-// 256 workgroups land 32 per XCD on 256 distinct CUs (the 157 KB of LDS a
-// workgroup takes leaves room for no second one on a CU). A cooperative
-// launch is not used: it costs ~18 us more per step to dispatch (405 vs
-// 387 us per config-2 step), and HIP serves it from a dedicated queue whose
-// teardown at process exit crashed every profiled run that had made one.
-// Should another kernel hold CUs during a step, the bounded waits give up
-// and the error is recorded in the workspace header; nothing hangs.
+// The placement probe at workspace initialisation is an ordinary launch;
+// it checks that the 256 workgroups land 32 per XCD on 256 distinct CUs (the
+// 157 KB of LDS a workgroup takes leaves room for no second one on a CU).
+// The steps are ordinary launches by default: a cooperative launch costs
+// ~18 us more per step to dispatch (405 vs 387 us per config-2 step), and
+// HIP serves it from a dedicated queue whose teardown at process exit
+// crashed every profiled run that had made one. Callers that share the GPU
+// with other work can ask for cooperative step launches
+// (gemma4_decode_step_set_cooperative), which the runtime admits only with
+// all workgroups resident. Otherwise, should another kernel hold CUs during
+// a step, the bounded waits give up and the error is recorded in the
+// workspace header; nothing hangs.
+std::atomic<int> g_cooperative{0};
+
 hipError_t launch_step(StepParams &p, hipStream_t stream) {
   void *args[] = {&p};
+  if (p.probe == nullptr && g_cooperative.load(std::memory_order_relaxed) != 0) {
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(decode_step_kernel),
+                                      dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds,
+                                      stream);
+  }
   return hipLaunchKernel(reinterpret_cast<const void *>(decode_step_kernel),
                          dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds, stream);
 }
@@ -1131,6 +1143,12 @@ extern "C" hipError_t gemma4_decode_step_status_async(const void *workspace, int
   if (workspace == nullptr || status == nullptr) return hipErrorInvalidValue;
   return hipMemcpyAsync(status, static_cast<const int32_t *>(workspace) + kHeaderError,
                         sizeof(int32_t), hipMemcpyDefault, stream);
+}
+
+extern "C" hipError_t gemma4_decode_step_set_cooperative(int32_t enable) {
+  if (enable != 0 && enable != 1) return hipErrorInvalidValue;
+  g_cooperative.store(enable, std::memory_order_relaxed);
+  return hipSuccess;
 }
 
 extern "C" hipError_t gemma4_decode_step_inject_stall(void *workspace, int32_t layer,

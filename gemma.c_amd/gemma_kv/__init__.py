@@ -110,6 +110,7 @@ SIGNATURES = {
     "gemma4_flash_attention_append_decode_paged_bf16_noalloc": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_decode_step_inject_stall": (_I32, [_P, _I32, ctypes.c_uint32, _P]),
+    "gemma4_decode_step_set_cooperative": (_I32, [_I32]),
     "gemma4_decode_step_layers_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _CFG, _P, _P, _P, _CFG, _P, _P, _I32, _I32, _F32,
                _I32, _P, ctypes.c_size_t, _P]),
@@ -307,6 +308,10 @@ def decode_step_status_async(workspace, status, stream=None) -> int:
     or pinned-host int32 tensor)."""
     return lib().gemma4_decode_step_status_async(ptr(workspace), ptr(status),
                                                  stream_handle(stream))
+
+
+def decode_step_set_cooperative(enable: bool) -> int:
+    return lib().gemma4_decode_step_set_cooperative(1 if enable else 0)
 
 
 def decode_step_inject_stall(workspace, layer: int, limit_ticks: int, stream=None) -> int:

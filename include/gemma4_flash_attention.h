@@ -259,6 +259,13 @@ hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t workspace_b
 hipError_t gemma4_decode_step_status(const void *workspace, int32_t *status);
 hipError_t gemma4_decode_step_status_async(const void *workspace, int32_t *status,
                                            hipStream_t stream);
+// Process-wide launch mode of the persistent step (no counterpart in the
+// reference): 0 (default) ordinary launches; 1 cooperative launches, which
+// the runtime admits only with all 256 workgroups resident -- for callers
+// that share the GPU with other kernels -- at ~18 us more dispatch cost per
+// step. (A process that has made a cooperative launch has been seen to
+// crash at exit under rocprofv3.)
+hipError_t gemma4_decode_step_set_cooperative(int32_t enable);
 // Fault injection for tests (no counterpart in the reference): from the next
 // launch on, at launch-relative layer `layer` one workgroup waits for a
 // workspace word that is never set, giving up after `limit_ticks` of the

@@ -245,6 +245,32 @@ def test_decode_step_failure_is_reported_and_sticky(dev):
         assert_close(got3[i], exp_out[i], f"layer {layer}")
 
 
+def test_decode_step_cooperative_launch_matches(dev):
+    """The optional cooperative launch mode runs the same kernel: same outputs
+    and caches as the ordinary launch, status 0."""
+    rng = np.random.default_rng(31)
+    first, count, seq, window, s_page, g_page = 0, 7, [151], 64, 1, 16
+    layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v = _case(
+        rng, first, count, seq, window, s_page, g_page)
+    pos = [n - 1 for n in seq]
+    scale = 1 / math.sqrt(DIM)
+    ws = _workspace(dev, 1)
+    results = []
+    for coop in (False, True):
+        dcaches = {n: to_dev(a, dev) for n, a in caches.items()}
+        gk.check(gk.decode_step_set_cooperative(coop), "set_cooperative")
+        try:
+            got = _run_step(dev, ws, layers, s_cfg, g_cfg, s_pt, g_pt, dcaches, q, k, v, seq,
+                            pos, scale)
+        finally:
+            gk.check(gk.decode_step_set_cooperative(False), "set_cooperative")
+        results.append((got, {n: from_dev_bf16(t) for n, t in dcaches.items()}))
+    assert np.array_equal(results[0][0], results[1][0])
+    for n in caches:
+        assert np.array_equal(results[0][1][n], results[1][1][n]), n
+    assert gk.lib().gemma4_decode_step_set_cooperative(2) != 0
+
+
 def test_decode_step_rejects_bad_arguments(dev):
     import torch
     rng = np.random.default_rng(1)
