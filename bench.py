@@ -836,13 +836,24 @@ def cpu_baseline(runs_1core: int = 3, runs_all: int = 5, quick: bool = False):
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it, with family / model / stepping
+    (some hosts report only a short model name)."""
+    fields = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping", "cpu MHz") and k not in fields:
+                    fields[k] = v
+            elif fields:
+                break
     except OSError:
         pass
-    return "unknown"
+    if not fields:
+        return "unknown"
+    extra = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping", "cpu MHz")
+                      if k in fields)
+    return f"{fields.get('model name', 'unknown')} ({extra})"
 
 
 def main():
