@@ -4,8 +4,9 @@ cache, each appending one token then attending, q/k/v ~ N(0,1) from a seed,
 scale 1/16.
 
 The loop is the reference decode loop for one layer: the runtime's decode-step
-bookkeeping (here its device-side form, which maps the ring slot, writes the
-token position and advances seq_len on the GPU) followed by the fused
+bookkeeping (its device-side form, which maps the ring slot, writes the token
+position and advances seq_len on the GPU, or the reference's host form with
+its uploads) followed by the fused
 append + split-K decode entry point, two launches per step, no host
 synchronisation between steps. The oracle runs the same 2048 steps on the
 CPU (ring bookkeeping, append, and the reference host attention of
@@ -30,7 +31,8 @@ def _checked(t):
     return t < 4 or t % 64 == 63 or t == STEPS - 1
 
 
-def test_config1_2048_sequential_steps(dev):
+@pytest.mark.parametrize("device_step", [True, False], ids=["device_step", "host_step"])
+def test_config1_2048_sequential_steps(dev, device_step):
     import torch
     rng = np.random.default_rng(2048)
     q = randn_bf16(rng, (STEPS, 1, QH, DIM))
@@ -55,13 +57,17 @@ def test_config1_2048_sequential_steps(dev):
     kv_row = HEADS * DIM * 2
     print(f"config1: {STEPS} steps, split {split} x {n}", flush=True)
     for t in range(STEPS):
-        gk.check(rt.prepare_decode_step_device(), f"device step {t}")
+        if device_step:
+            gk.check(rt.prepare_decode_step_device(), f"device step {t}")
+        else:
+            gk.check(rt.prepare_decode_step(), f"host step {t}")
         gk.check(gk.flash_attention_append_decode_paged_bf16(
             out.data_ptr() + t * row, pm, pl, pa, dq.data_ptr() + t * row, ck, cv, pt, seq, pos,
             dk.data_ptr() + t * kv_row, dv.data_ptr() + t * kv_row, cfg, 0, scale, split, n, 1),
             f"append_decode step {t}")
     torch.cuda.synchronize()
-    assert rt.device_step_status() == 0
+    if device_step:
+        assert rt.device_step_status() == 0
     got = from_dev_bf16(out)
 
     # Oracle: the same 2048 steps on the CPU.
