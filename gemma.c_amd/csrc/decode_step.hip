@@ -435,15 +435,24 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     // waits, with the given limit, for a header word the host never sets.
     const int32_t stall_layer = wave_uniform(s_stall_layer);
     const uint64_t stall_ticks = (uint32_t)wave_uniform(s_stall_ticks);
-    // Layer `layer_i` is complete once all 8 XCD flags read `epoch`.
-    auto wait_layer_device = [&](int32_t layer_i) {
-      const int32_t *row = p.global_flags + layer_i * kGlobalFlagStride;
+    // Polls a flag word per lane until every lane reads `epoch`, one load
+    // in flight at a time (keeping up to four in flight measured no faster:
+    // the flag's propagation, not the poll spacing, sets the wait).
+    auto poll = [&](auto load) {
       const uint64_t t0 = now_ticks();
       while (!abort) {
-        const bool ok = lane >= kXcds || coherent_load_i32(row + lane) == epoch;
-        if (__ballot(!ok) == 0) break;
+        if (__ballot(load() != epoch) == 0) return;
         if (now_ticks() - t0 > kWaitTicks) fail(1);
       }
+    };
+    // Layer `layer_i` is complete once all 8 XCD flags read `epoch`.
+    const BufferRsrc flag_buf =
+        buffer_of(p.global_flags, (int64_t)kNumModelLayers * kGlobalFlagStride * 4);
+    auto wait_layer_device = [&](int32_t layer_i) {
+      const int32_t off = (layer_i * kGlobalFlagStride + (lane & (kXcds - 1))) * 4;
+      poll([&] {
+        return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(flag_buf, off, 0, kCoherentAux);
+      });
     };
     // Ticket 0 of each XCD polls the 8 device flags and raises the XCD's
     // go flag in its L2; the other 31 workgroups poll that (an L2 round
@@ -456,12 +465,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)epoch, go_buf, off, 0, 0);
         return;
       }
-      const uint64_t t0 = now_ticks();
-      while (!abort) {
-        const int32_t v = (int32_t)__builtin_amdgcn_raw_buffer_load_b32(go_buf, off, 0, kLocalLoadAux);
-        if (v == epoch) break;
-        if (now_ticks() - t0 > kWaitTicks) fail(1);
-      }
+      poll([&] {
+        return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(go_buf, off, 0, kLocalLoadAux);
+      });
     };
     // Ticket 0 of each XCD: collect the XCD's 32 local flags, then raise
     // the XCD's device-wide flag.
@@ -469,14 +475,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         buffer_of(p.local_flags, (int64_t)kNumModelLayers * kXcds * kXcdSlots * 4);
     auto publish_xcd = [&](int32_t layer_i) {
       const int32_t off = ((layer_i * kXcds + xcd) * kXcdSlots + (lane & (kXcdSlots - 1))) * 4;
-      const uint64_t t0 = now_ticks();
-      while (!abort) {
-        const bool ok = lane >= kXcdSlots ||
-                        (int32_t)__builtin_amdgcn_raw_buffer_load_b32(local_buf, off, 0,
-                                                                      kLocalLoadAux) == epoch;
-        if (__ballot(!ok) == 0) break;
-        if (now_ticks() - t0 > kWaitTicks) fail(1);
-      }
+      poll([&] {
+        return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(local_buf, off, 0, kLocalLoadAux);
+      });
       if (lane == 0) coherent_store_i32(p.global_flags + layer_i * kGlobalFlagStride + xcd, epoch);
     };
     // Lane (g, sp) = (lane / 32, lane % 32) reads split sp's row g, so the
