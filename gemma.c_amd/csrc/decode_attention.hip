@@ -70,6 +70,9 @@ struct DecodeParams {
   float q_scale;  // softmax_scale * log2(e)
   int32_t split_size;
   int32_t num_splits;
+  // Non-null (persistent decode step only): a nonzero word here turns the
+  // launch into zeros for its output rows, with no append.
+  const int32_t *gate;
 };
 
 template <int kHeads, int kDim, int kHeadsPerWave, int kLoads, int kChunkTiles>
@@ -249,6 +252,17 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
   const int32_t key_count = seq_len > first ? seq_len - first : 0;
   const int32_t live_splits = (key_count + p.split_size - 1) / p.split_size;
   const bool direct = p.num_splits == 1;
+
+  if (p.gate != nullptr && wave_uniform(*p.gate) != 0) {
+    // A failed step: no append; a direct launch zeroes its rows (the
+    // combine kernel zeroes them otherwise).
+    if (direct && split == 0) {
+      uint16_t *rows = p.out + ((int64_t)b * kQueryHeads + head * G) * D;
+      for (int e = threadIdx.x; e < G * D / kPackElems; e += blockDim.x)
+        store128(rows + e * kPackElems, make_uint4(0, 0, 0, 0));
+    }
+    return;
+  }
 
   // ---- fused append of the current token (one split per (b, head) owns it)
   int32_t new_pos = -1, new_row = -1;
@@ -694,13 +708,18 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
     uint16_t *__restrict__ out, const float *__restrict__ partial_m,
     const float *__restrict__ partial_l, const float *__restrict__ partial_acc,
     const int32_t *__restrict__ seq_lengths, int32_t window_size,
-    int32_t split_size, int32_t num_splits) {
+    int32_t split_size, int32_t num_splits, const int32_t *__restrict__ gate) {
   __shared__ float s_w[kCombineChunk];
   __shared__ float s_tmp[kCombineThreads / kWave];
   __shared__ float s_acc[16][kCombineDims];
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int dim0 = blockIdx.y * kCombineDims;
+  if (gate != nullptr && *gate != 0) {  // a failed persistent step: zeros
+    if (t < kCombineDims / 4)
+      *reinterpret_cast<uint2 *>(out + row * kDim + dim0 + t * 4) = make_uint2(0, 0);
+    return;
+  }
   const int32_t b = (int32_t)(row / kQueryHeads);
   const int32_t seq_len = seq_lengths[b];
   int32_t first = window_size > 0 ? seq_len - window_size : 0;
@@ -798,7 +817,7 @@ hipError_t launch_decode(const DecodeParams &p, int32_t batch_count, bool combin
                      dim3(batch_count * kQueryHeads, D / kCombineDims),
                      dim3(kCombineThreads), 0, stream, p.out, p.partial_m, p.partial_l,
                      p.partial_acc, p.seq_lengths, p.c.window_size, p.split_size,
-                     p.num_splits);
+                     p.num_splits, p.gate);
   return hipGetLastError();
 }
 
@@ -812,7 +831,7 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
                         int32_t num_splits, int32_t batch_count, bool combine,
                         hipStream_t stream, const uint16_t *q_norm_weight = nullptr,
                         const uint16_t *k_norm_weight = nullptr, const float *cos = nullptr,
-                        const float *sin = nullptr) {
+                        const float *sin = nullptr, const int32_t *gate = nullptr) {
   if (batch_count == 0) return hipSuccess;
   if (batch_count < 0 || batch_count > c.batch_size || batch_count > 65535 || num_splits > 65535 ||
       !valid_decode_config(c, layer) || !(softmax_scale > 0.0f) ||
@@ -847,6 +866,7 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
   p.q_scale = softmax_scale * kLog2e;
   p.split_size = split_size;
   p.num_splits = num_splits;
+  p.gate = gate;
   if (c.num_heads == 8 && c.head_dim == 256) {
     return launch_decode<SlidingShape>(p, batch_count, combine, stream);
   }
@@ -880,6 +900,22 @@ hipError_t noalloc_scratch(float **out) {
 }
 
 }  // namespace
+
+hipError_t decode_append_gated(uint16_t *out, float *pm, float *pl, float *pacc,
+                               const uint16_t *q, uint16_t *cache_k, uint16_t *cache_v,
+                               const int32_t *page_table, const int32_t *seq_lengths,
+                               const int32_t *token_position, const uint16_t *new_k,
+                               const uint16_t *new_v, const Gemma4KvCacheConfig &c,
+                               int32_t layer, float softmax_scale, int32_t split_size,
+                               int32_t num_splits, int32_t batch_count, const int32_t *gate,
+                               hipStream_t stream) {
+  if (token_position == nullptr || new_k == nullptr || gate == nullptr) return hipErrorInvalidValue;
+  return decode_entry(out, pm, pl, pacc, q, cache_k, cache_v, page_table, seq_lengths,
+                      token_position, new_k, new_v, nullptr, c, layer, softmax_scale, split_size,
+                      num_splits, batch_count, /*combine=*/true, stream, nullptr, nullptr, nullptr,
+                      nullptr, gate);
+}
+
 }  // namespace gemma4
 
 using namespace gemma4;
@@ -1018,11 +1054,13 @@ hipError_t gemma4_flash_attention_decode_combine_bf16(
   if (config.head_dim == 256) {
     hipLaunchKernelGGL(decode_combine_kernel<256>, dim3(batch_count * kQueryHeads, 256 / kCombineDims),
                        block, 0, stream, out, d_partial_m, d_partial_l, d_partial_acc,
-                       d_seq_lengths, config.window_size, split_size, num_splits);
+                       d_seq_lengths, config.window_size, split_size, num_splits,
+                       static_cast<const int32_t *>(nullptr));
   } else if (config.head_dim == 512) {
     hipLaunchKernelGGL(decode_combine_kernel<512>, dim3(batch_count * kQueryHeads, 512 / kCombineDims),
                        block, 0, stream, out, d_partial_m, d_partial_l, d_partial_acc,
-                       d_seq_lengths, config.window_size, split_size, num_splits);
+                       d_seq_lengths, config.window_size, split_size, num_splits,
+                       static_cast<const int32_t *>(nullptr));
   } else {
     return hipErrorInvalidValue;
   }

@@ -153,4 +153,17 @@ __device__ __forceinline__ auto coherent_view(const float *p, int32_t count) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), 0, count * 4, 0x00020000);
 }
 
+// The fused append + split-K decode with the separate combine
+// (decode_attention.hip) for the persistent step's 1 x 512 global layers:
+// while the word at `gate` (the step workspace's status) is nonzero the
+// launches append nothing and write zeros to `out`.
+hipError_t decode_append_gated(uint16_t *out, float *pm, float *pl, float *pacc,
+                               const uint16_t *q, uint16_t *cache_k, uint16_t *cache_v,
+                               const int32_t *page_table, const int32_t *seq_lengths,
+                               const int32_t *token_position, const uint16_t *new_k,
+                               const uint16_t *new_v, const Gemma4KvCacheConfig &c,
+                               int32_t layer, float softmax_scale, int32_t split_size,
+                               int32_t num_splits, int32_t batch_count, const int32_t *gate,
+                               hipStream_t stream);
+
 }  // namespace gemma4

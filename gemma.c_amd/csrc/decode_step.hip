@@ -1014,8 +1014,9 @@ WorkspaceLayout workspace_layout(int32_t batch_count) {
   return w;
 }
 
-// Per-device result of the placement probe: 0 unknown, 1 ok, -1 unsupported.
-int g_placement_ok[64];
+// Per-device result of the placement probe: 0 unknown, 1 ok, -1 unsupported
+// (atomic: workspace_init and the steps may run on different host threads).
+std::atomic<int> g_placement_ok[64];
 
 StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_count) {
   StepParams p{};
@@ -1098,7 +1099,7 @@ extern "C" hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t 
   e = hipGetDevice(&device);
   if (e != hipSuccess) return e;
   if (device < 0 || device >= 64) return hipErrorNotSupported;
-  if (g_placement_ok[device] == 0) {
+  if (g_placement_ok[device].load() == 0) {
     e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_step_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPadLds);
     if (e != hipSuccess) return e;
@@ -1125,9 +1126,9 @@ extern "C" hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t 
       ++count[x];
     }
     for (int x = 0; x < kXcds; ++x) ok &= count[x] == kXcdSlots;
-    g_placement_ok[device] = ok ? 1 : -1;
+    g_placement_ok[device].store(ok ? 1 : -1);
   }
-  return g_placement_ok[device] == 1 ? hipSuccess : hipErrorNotSupported;
+  return g_placement_ok[device].load() == 1 ? hipSuccess : hipErrorNotSupported;
 }
 
 extern "C" hipError_t gemma4_decode_step_status(const void *workspace, int32_t *status) {
@@ -1228,7 +1229,7 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
     return hipErrorInvalidValue;
   int device = 0;
   if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64 ||
-      g_placement_ok[device] != 1)
+      g_placement_ok[device].load() != 1)
     return hipErrorNotSupported;  // gemma4_decode_step_workspace_init first
   gemma4_bf16 *const ck[2] = {sliding_cache_k, global_cache_k};
   gemma4_bf16 *const cv[2] = {sliding_cache_v, global_cache_v};
@@ -1244,9 +1245,10 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
                     scale, batch_count, workspace, stream);
   }
   // Reference global geometry: runs of sliding layers go to the persistent
-  // kernel, each global layer to one fused append + split-K launch with the
-  // in-kernel combine (its partials and counters in the workspace). Stream
-  // order keeps layer i after layer i-1. Rows are laid out back to back,
+  // kernel, each global layer to one fused append + split-K launch and the
+  // combine kernel (its partials in the workspace), gated by the workspace
+  // status like the persistent launches. Stream order keeps layer i after
+  // layer i-1. Rows are laid out back to back,
   // layer by layer, each layer's [batch][16][head_dim] (q, out) and
   // [batch][Hk][head_dim] (k, v) at its own width.
   int32_t ref_split = 0, ref_splits = 0;
@@ -1275,13 +1277,12 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
   for (int32_t l = first_layer; l < last;) {
     if (is_global(l)) {
       const int64_t slots = rows * ref_splits;
-      const hipError_t e = gemma4_flash_attention_append_decode_paged_bf16(
-          reinterpret_cast<gemma4_bf16 *>(op), ref_partials, ref_partials + slots,
-          ref_partials + 2 * slots, reinterpret_cast<const gemma4_bf16 *>(qp),
-          global_cache_k, global_cache_v, global_page_table, seq_lengths, token_position,
-          reinterpret_cast<const gemma4_bf16 *>(kp), reinterpret_cast<const gemma4_bf16 *>(vp),
-          nullptr, global_config, gemma4_kv_cache_layer_index(l, true), scale,
-          ref_split, ref_splits, batch_count, stream);
+      const hipError_t e = decode_append_gated(
+          op, ref_partials, ref_partials + slots, ref_partials + 2 * slots, qp,
+          reinterpret_cast<uint16_t *>(global_cache_k),
+          reinterpret_cast<uint16_t *>(global_cache_v), global_page_table, seq_lengths,
+          token_position, kp, vp, global_config, gemma4_kv_cache_layer_index(l, true), scale,
+          ref_split, ref_splits, batch_count, ints + kHeaderError, stream);
       if (e != hipSuccess) return e;
       qp += rows * kRefDim;
       op += rows * kRefDim;

@@ -241,12 +241,11 @@ hipError_t gemma4_decode_prep_append_bf16(
 // that the workgroups land one per CU, 32 per XCD; hipErrorNotSupported
 // otherwise), then reuse it for every step (stream order). Calls sharing a
 // workspace must not overlap.
-// With the 1 x 512 global geometry the global layers' launches are not gated
-// by the status below (only the persistent launches are).
 // Failure is stream-ordered and sticky: every wait of the step is bounded
 // (0.2 s); if one gives up (another kernel held CUs), the launch writes
 // zeros for the output chunks whose wait gave up and records a nonzero
-// status in the workspace; every later launch on that workspace then writes
+// status in the workspace; every later launch on that workspace (with the
+// 1 x 512 global geometry also the global layers' launches) then writes
 // zeros to all of its outputs, appends nothing and returns at once, until
 // gemma4_decode_step_workspace_init is called again. Status codes: 0 ok, 1 a
 // wait gave up, 2 a split exceeded the 512-key row table.

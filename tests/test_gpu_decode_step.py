@@ -131,15 +131,10 @@ REF_CASES = [
 ]
 
 
-@pytest.mark.parametrize("first,count,seq,window,s_page,g_page", REF_CASES)
-def test_decode_step_reference_global_geometry(dev, first, count, seq, window, s_page, g_page):
-    """The reference model's own geometry (src/gemma4.h:17-21): sliding layers
-    8 x 256, global layers 1 KV head x 512 (GQA 16). Rows of q/k/v/out are laid
-    out layer by layer at each layer's width. Checked against the oracle
-    applied layer by layer: caches bit-exact, outputs within tolerance; a
-    second step on the same workspace gives the same outputs."""
-    import torch
-    rng = np.random.default_rng(sum(seq) * 3 + first + count)
+def _ref_case(rng, first, count, seq, window, s_page, g_page):
+    """Inputs and oracle results of a step in the reference model's geometry
+    (sliding 8 x 256, global 1 x 512); q/k/v rows flattened layer by layer at
+    each layer's width."""
     batch = len(seq)
     layers = list(range(first, first + count))
     n_s = sum(1 for l in range(48) if not is_global(l))
@@ -172,30 +167,88 @@ def test_decode_step_reference_global_geometry(dev, first, count, seq, window, s
         oracle.kv_cache_write(ck, cv, cfg, pt, list(range(batch)), pos, cl, ks[i], vs[i])
         exp_out.append(oracle.decode_attention(qs[i], ck, cv, pt, seq, cfg, cl, scale))
     flat = lambda arrs: np.concatenate([a.reshape(-1) for a in arrs])
-    d = {n: to_dev(a, dev) for n, a in caches.items()}
-    dq, dk, dv = to_dev(flat(qs), dev), to_dev(flat(ks), dev), to_dev(flat(vs), dev)
-    ws = _workspace(dev, batch)
-    outs = []
-    for rep in range(2):
-        out = torch.zeros(sum(batch * 16 * dd for _, dd in geo), dtype=torch.int16, device=dev)
-        gk.check(gk.decode_step_layers_bf16(
-            out, dq, dk, dv, d["sk"], d["sv"], to_dev(s_pt, dev), gk.make_config(*s_cfg),
-            d["gk"], d["gv"], to_dev(g_pt, dev), gk.make_config(*g_cfg),
-            to_dev(np.asarray(seq, np.int32), dev), to_dev(np.asarray(pos, np.int32), dev),
-            first, count, scale, batch, ws), "decode_step 1x512")
-        torch.cuda.synchronize()
-        assert gk.decode_step_status(ws) == 0
-        outs.append(from_dev_bf16(out))
-        if rep == 0:
-            for n in caches:
-                assert np.array_equal(from_dev_bf16(d[n]).reshape(caches[n].shape), exp[n]), n
-    assert np.array_equal(outs[0], outs[1])
-    off = 0
-    for i, layer in enumerate(layers):
-        size = batch * 16 * geo[i][1]
-        assert_close(outs[0][off:off + size].reshape(batch, 16, geo[i][1]), exp_out[i],
-                     f"layer {layer}")
-        off += size
+    return dict(layers=layers, geo=geo, s_cfg=s_cfg, g_cfg=g_cfg, s_pt=s_pt, g_pt=g_pt,
+                caches=caches, q=flat(qs), k=flat(ks), v=flat(vs), seq=seq, pos=pos,
+                scale=scale, exp=exp, exp_out=exp_out)
+
+
+def _ref_run(dev, ws, c, d, expect_status=0, fill=0):
+    """One step of a _ref_case on device caches `d`; returns the output rows
+    as a list per layer ([batch][16][width])."""
+    import torch
+    batch = len(c["seq"])
+    total = sum(batch * 16 * w for _, w in c["geo"])
+    out = torch.full((total,), fill, dtype=torch.int16, device=dev)
+    gk.check(gk.decode_step_layers_bf16(
+        out, to_dev(c["q"], dev), to_dev(c["k"], dev), to_dev(c["v"], dev), d["sk"], d["sv"],
+        to_dev(c["s_pt"], dev), gk.make_config(*c["s_cfg"]), d["gk"], d["gv"],
+        to_dev(c["g_pt"], dev), gk.make_config(*c["g_cfg"]),
+        to_dev(np.asarray(c["seq"], np.int32), dev), to_dev(np.asarray(c["pos"], np.int32), dev),
+        c["layers"][0], len(c["layers"]), c["scale"], batch, ws), "decode_step 1x512")
+    torch.cuda.synchronize()
+    assert gk.decode_step_status(ws) == expect_status
+    flat = from_dev_bf16(out)
+    rows, off = [], 0
+    for _, w in c["geo"]:
+        rows.append(flat[off:off + batch * 16 * w].reshape(batch, 16, w))
+        off += batch * 16 * w
+    return rows
+
+
+@pytest.mark.parametrize("first,count,seq,window,s_page,g_page", REF_CASES)
+def test_decode_step_reference_global_geometry(dev, first, count, seq, window, s_page, g_page):
+    """The reference model's own geometry (src/gemma4.h:17-21): sliding layers
+    8 x 256, global layers 1 KV head x 512 (GQA 16). Rows of q/k/v/out are laid
+    out layer by layer at each layer's width. Checked against the oracle
+    applied layer by layer: caches bit-exact, outputs within tolerance; a
+    second step on the same workspace gives the same outputs."""
+    c = _ref_case(np.random.default_rng(sum(seq) * 3 + first + count), first, count, seq,
+                  window, s_page, g_page)
+    d = {n: to_dev(a, dev) for n, a in c["caches"].items()}
+    ws = _workspace(dev, len(seq))
+    first_rows = _ref_run(dev, ws, c, d)
+    for n in c["caches"]:
+        assert np.array_equal(from_dev_bf16(d[n]).reshape(c["caches"][n].shape), c["exp"][n]), n
+    again = _ref_run(dev, ws, c, d)
+    for i, layer in enumerate(c["layers"]):
+        assert np.array_equal(again[i], first_rows[i]), f"layer {layer}"
+        assert_close(first_rows[i], c["exp_out"][i], f"layer {layer}")
+
+
+def test_decode_step_failure_sticky_reference_geometry(dev):
+    """Sticky failure with the 1 x 512 global geometry, where global layers run
+    as separate launches between the persistent runs: a wait made to give up
+    at layer 2 (fault injection, limit 20 us) fails the step; the global
+    layer 5 and the persistent run after it then write zeros and append
+    nothing (the global cache stays as it was); the next step on the
+    workspace writes only zeros and leaves every cache untouched; after
+    workspace_init the step is correct again."""
+    import torch
+    c = _ref_case(np.random.default_rng(512), 0, 7, [151], 64, 1, 16)
+    d = {n: to_dev(a, dev) for n, a in c["caches"].items()}
+    ws = _workspace(dev, 1)
+    gk.check(gk.decode_step_inject_stall(ws, 2, 2000), "inject_stall")
+    print("decode step 1x512: stalled launch", flush=True)
+    got1 = _ref_run(dev, ws, c, d, expect_status=1, fill=0x1234)
+    assert c["layers"][5] == 5 and c["geo"][5] == (1, 512)
+    assert not got1[5].any() and not got1[6].any()
+    assert np.array_equal(from_dev_bf16(d["gk"]).reshape(c["caches"]["gk"].shape),
+                          c["caches"]["gk"])
+    assert np.array_equal(from_dev_bf16(d["gv"]).reshape(c["caches"]["gv"].shape),
+                          c["caches"]["gv"])
+    snap = {n: t.clone() for n, t in d.items()}
+    print("decode step 1x512: launch on the failed workspace", flush=True)
+    got2 = _ref_run(dev, ws, c, d, expect_status=1, fill=0x1234)
+    assert not any(r.any() for r in got2)
+    for n in d:
+        assert torch.equal(d[n], snap[n]), n
+    gk.check(gk.decode_step_workspace_init(ws, 1), "workspace_init")
+    d = {n: to_dev(a, dev) for n, a in c["caches"].items()}
+    got3 = _ref_run(dev, ws, c, d)
+    for n in c["caches"]:
+        assert np.array_equal(from_dev_bf16(d[n]).reshape(c["caches"][n].shape), c["exp"][n]), n
+    for i, layer in enumerate(c["layers"]):
+        assert_close(got3[i], c["exp_out"][i], f"layer {layer}")
 
 
 def test_decode_step_failure_is_reported_and_sticky(dev):
