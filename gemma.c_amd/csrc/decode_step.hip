@@ -322,9 +322,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     return;
   }
 
-  // Wave-local tile j of a split is tile t = wave + 4 j; tiles 0..15 are
-  // prefetched into compute-wave registers, tiles 16 .. 16 + kLdsSlots - 1
-  // of a global layer come from LDS slot t - 16, later ones are streamed.
+  // Wave-local tile j of a split is tile t = wave + kComputeWaves * j; tiles
+  // 0 .. kRegTiles - 1 are prefetched into compute-wave registers, tiles
+  // kRegTiles .. kRegTiles + kLdsSlots - 1 of a global layer come from LDS
+  // slot t - kRegTiles, later ones are streamed.
   if (wave == kPrefetchWave) {
     // ----------------------------------------------------------- prefetch
     // The LDS tiles of the next global layer are requested a few slots at a
