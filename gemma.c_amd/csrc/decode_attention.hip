@@ -46,34 +46,6 @@ namespace {
 
 constexpr int kMaxWaves = 4;
 
-struct DecodeParams {
-  uint16_t *out;
-  float *partial_m;
-  float *partial_l;
-  float *partial_acc;
-  const uint16_t *q;
-  uint16_t *cache_k;  // written only by the fused append
-  uint16_t *cache_v;
-  const int32_t *page_table;
-  const int32_t *seq_lengths;
-  const int32_t *token_position;  // null: no append
-  int32_t *counters;              // null: separate combine kernel
-  const uint16_t *new_k;
-  const uint16_t *new_v;
-  // Fused preparation (null q_norm_weight: q and the new K/V come prepared).
-  const uint16_t *q_norm_weight;
-  const uint16_t *k_norm_weight;
-  const float *cos;              // [position][rotary / 2]
-  const float *sin;
-  Gemma4KvCacheConfig c;
-  int32_t layer;
-  float q_scale;  // softmax_scale * log2(e)
-  int32_t split_size;
-  int32_t num_splits;
-  // Non-null (persistent decode step only): a nonzero word here turns the
-  // launch into zeros for its output rows, with no append.
-  const int32_t *gate;
-};
 
 template <int kHeads, int kDim, int kHeadsPerWave, int kLoads, int kChunkTiles>
 struct DecodeShape {
@@ -269,9 +241,11 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
   const bool prep = p.q_norm_weight != nullptr;
   if (p.token_position != nullptr) {
     new_pos = wave_uniform(p.token_position[b]);
-    new_row = wave_uniform(append_row(c, p.page_table, p.layer, b, new_pos));
     const bool in_live = new_pos >= first && new_pos < seq_len;
     const int32_t owner = in_live ? (new_pos - first) / p.split_size : 0;
+    // Only the owning split needs the cache row (a dependent page-table
+    // load); no other split's key range holds the new token.
+    new_row = split == owner ? wave_uniform(append_row(c, p.page_table, p.layer, b, new_pos)) : -1;
     const bool writes = split == owner && new_row >= 0;
     if (prep) {
       // Wave 0 prepares the token's K and V rows (both lane rows compute, the
@@ -672,36 +646,14 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
 // Log-sum-exp combine of the live splits of one (batch, query head) row
 // (src/gemma4_flash_attention_decode.cu:880-977), as a separate launch.
 // Workgroup (row, 64-dim block): 256 threads = 16 split lanes x 16 groups of
-// 4 dims. The split maxima come first (all threads, strided over splits); the
-// weights of a chunk of up to kCombineChunk splits go to LDS, every thread
-// accumulates its splits' float4 partials, and the 16 split lanes are summed
-// through LDS.
+// 4 dims. Each thread folds its splits (s = lane, lane + 16, ...) into a
+// running (max, sum, acc) as it streams them -- the loads do not depend on
+// the arithmetic, so they are all in flight together -- and the 16 split
+// lanes are merged the same way through LDS. Empty splits (l = 0) weigh 0;
+// a row without a live split is zeros.
 constexpr int kCombineThreads = 256;
-constexpr int kCombineChunk = 1024;
 constexpr int kCombineDims = 64;
-
-__device__ __forceinline__ float block_reduce_max(float v, float *s_tmp) {
-  v = reduce_max_from<1>(v);
-  const int wave = threadIdx.x / kWave;
-  __syncthreads();
-  if (__lane_id() == 0) s_tmp[wave] = v;
-  __syncthreads();
-  float r = s_tmp[0];
-#pragma unroll
-  for (int w = 1; w < kCombineThreads / kWave; ++w) r = fmaxf(r, s_tmp[w]);
-  return r;
-}
-__device__ __forceinline__ float block_reduce_sum(float v, float *s_tmp) {
-  v = reduce_sum_from<1>(v);
-  const int wave = threadIdx.x / kWave;
-  __syncthreads();
-  if (__lane_id() == 0) s_tmp[wave] = v;
-  __syncthreads();
-  float r = s_tmp[0];
-#pragma unroll
-  for (int w = 1; w < kCombineThreads / kWave; ++w) r += s_tmp[w];
-  return r;
-}
+constexpr int kCombineLanes = kCombineThreads / (kCombineDims / 4);  // split lanes
 
 template <int kDim>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
@@ -709,9 +661,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
     const float *__restrict__ partial_l, const float *__restrict__ partial_acc,
     const int32_t *__restrict__ seq_lengths, int32_t window_size,
     int32_t split_size, int32_t num_splits, const int32_t *__restrict__ gate) {
-  __shared__ float s_w[kCombineChunk];
-  __shared__ float s_tmp[kCombineThreads / kWave];
-  __shared__ float s_acc[16][kCombineDims];
+  __shared__ float s_m[kCombineLanes], s_l[kCombineLanes];
+  __shared__ float4 s_a[kCombineLanes][kCombineDims / 4];
   const int t = threadIdx.x;
   const int64_t row = blockIdx.x;
   const int dim0 = blockIdx.y * kCombineDims;
@@ -728,56 +679,57 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
   int32_t splits = (key_count + split_size - 1) / split_size;
   splits = splits < num_splits ? splits : num_splits;
 
+  const int sl = t / (kCombineDims / 4);  // split lane
+  const int dg = t % (kCombineDims / 4);  // 4-dim group
   const float *pm = partial_m + row * num_splits;
   const float *pl = partial_l + row * num_splits;
-  const float *pa = partial_acc + row * num_splits * kDim + dim0;
-  float mloc = -INFINITY;
-  for (int32_t s = t; s < splits; s += kCombineThreads) mloc = fmaxf(mloc, pm[s]);
-  const float big_m = block_reduce_max(mloc, s_tmp);
-
-  const int dg = t % 16;   // 4-dim group
-  const int sl = t / 16;   // split lane
-  float lloc = 0.0f;
+  const float *pa = partial_acc + row * num_splits * kDim + dim0 + dg * 4;
+  float big_m = -INFINITY, big_l = 0.0f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int32_t c0 = 0; c0 < splits; c0 += kCombineChunk) {
-    const int32_t cn = min(kCombineChunk, splits - c0);
-    for (int32_t s = t; s < cn; s += kCombineThreads) {
-      const float ls = pl[c0 + s];
-      const float w = ls > 0.0f ? __builtin_amdgcn_exp2f((pm[c0 + s] - big_m) * kLog2e) : 0.0f;
-      s_w[s] = w;
-      lloc = fmaf(ls > 0.0f ? ls : 0.0f, w, lloc);
-    }
-    __syncthreads();
 #pragma unroll 4
-    for (int32_t s = sl; s < cn; s += 16) {
-      const float w = s_w[s];
-      if (w != 0.0f) {
-        const float4 a = *reinterpret_cast<const float4 *>(pa + (int64_t)(c0 + s) * kDim + dg * 4);
-        acc.x = fmaf(a.x, w, acc.x);
-        acc.y = fmaf(a.y, w, acc.y);
-        acc.z = fmaf(a.z, w, acc.z);
-        acc.w = fmaf(a.w, w, acc.w);
-      }
-    }
-    __syncthreads();
+  for (int32_t s = sl; s < splits; s += kCombineLanes) {
+    const float ms = pm[s];
+    const float ls = pl[s];
+    const float4 raw = *reinterpret_cast<const float4 *>(pa + (int64_t)s * kDim);
+    const bool live = ls > 0.0f;
+    // An empty split's acc is never used, whatever it holds.
+    const float4 a = live ? raw : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float m_new = live ? fmaxf(big_m, ms) : big_m;
+    const float f_old = big_m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((big_m - m_new) * kLog2e);
+    const float f_new = live ? __builtin_amdgcn_exp2f((ms - m_new) * kLog2e) : 0.0f;
+    big_l = fmaf(ls > 0.0f ? ls : 0.0f, f_new, big_l * f_old);
+    acc.x = fmaf(a.x, f_new, acc.x * f_old);
+    acc.y = fmaf(a.y, f_new, acc.y * f_old);
+    acc.z = fmaf(a.z, f_new, acc.z * f_old);
+    acc.w = fmaf(a.w, f_new, acc.w * f_old);
+    big_m = m_new;
   }
-  const float big_l = block_reduce_sum(lloc, s_tmp);
-  s_acc[sl][dg * 4 + 0] = acc.x;
-  s_acc[sl][dg * 4 + 1] = acc.y;
-  s_acc[sl][dg * 4 + 2] = acc.z;
-  s_acc[sl][dg * 4 + 3] = acc.w;
+  if (dg == 0) {
+    s_m[sl] = big_m;
+    s_l[sl] = big_l;
+  }
+  s_a[sl][dg] = acc;
   __syncthreads();
   if (t < kCombineDims / 4) {
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < kCombineLanes; ++k) m = fmaxf(m, s_m[k]);
+    float l = 0.0f;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) v[j] += s_acc[k][t * 4 + j];
+    for (int k = 0; k < kCombineLanes; ++k) {
+      const float f = s_m[k] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f((s_m[k] - m) * kLog2e);
+      l = fmaf(s_l[k], f, l);
+      const float4 v = s_a[k][t];
+      a.x = fmaf(v.x, f, a.x);
+      a.y = fmaf(v.y, f, a.y);
+      a.z = fmaf(v.z, f, a.z);
+      a.w = fmaf(v.w, f, a.w);
     }
-    const float inv = (splits > 0 && big_l > 0.0f) ? 1.0f / big_l : 0.0f;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     uint2 o;
-    o.x = pack_bf16x2(v[0] * inv, v[1] * inv);
-    o.y = pack_bf16x2(v[2] * inv, v[3] * inv);
+    o.x = pack_bf16x2(a.x * inv, a.y * inv);
+    o.y = pack_bf16x2(a.z * inv, a.w * inv);
     *reinterpret_cast<uint2 *>(out + row * kDim + dim0 + t * 4) = o;
   }
 }

@@ -4,8 +4,39 @@
 #pragma once
 
 #include "gemma4_device.hpp"
+#include "gemma4_kv_cache.h"
 
 namespace gemma4 {
+
+// Arguments of the split-K decode kernels (decode_attention.hip).
+struct DecodeParams {
+  uint16_t *out;
+  float *partial_m;
+  float *partial_l;
+  float *partial_acc;
+  const uint16_t *q;
+  uint16_t *cache_k;  // written only by the fused append
+  uint16_t *cache_v;
+  const int32_t *page_table;
+  const int32_t *seq_lengths;
+  const int32_t *token_position;  // null: no append
+  int32_t *counters;              // null: separate combine kernel
+  const uint16_t *new_k;
+  const uint16_t *new_v;
+  // Fused preparation (null q_norm_weight: q and the new K/V come prepared).
+  const uint16_t *q_norm_weight;
+  const uint16_t *k_norm_weight;
+  const float *cos;              // [position][rotary / 2]
+  const float *sin;
+  Gemma4KvCacheConfig c;
+  int32_t layer;
+  float q_scale;  // softmax_scale * log2(e)
+  int32_t split_size;
+  int32_t num_splits;
+  // Non-null (persistent decode step only): a nonzero word here turns the
+  // launch into zeros for its output rows, with no append.
+  const int32_t *gate;
+};
 
 constexpr int kRowInvalid = -1;   // key outside the split or unmapped page
 constexpr int kRowNewToken = -2;  // key being appended in this launch

@@ -163,6 +163,55 @@ def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, wi
     assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
 
 
+D512_EDGES = [
+    # seq_lengths, split_size, num_splits, unmapped pages, outliers
+    ([8193], 64, 129, (), False),           # 64-key splits
+    ([1000, 257], 256, 4, (), False),       # long splits, ragged batch
+    ([4100], 512, 9, (5, 17, 30), False),   # unmapped pages inside splits
+    ([8192], 128, 64, (), True),            # 1% of keys x8: the running maximum moves
+    ([17], 16, 2, (), False),               # a split of one key
+]
+
+
+@pytest.mark.parametrize("seq,split_size,num_splits,holes,outliers", D512_EDGES)
+def test_decode_1x512_edges(dev, seq, split_size, num_splits, holes, outliers):
+    """Edge cases of the reference model's global geometry (1 KV head x 512,
+    16 query heads): fused append of the last token against the oracle's
+    append-then-attend, caches bit-exact and outputs within the north-star
+    tolerance; the unfused call on the appended cache gives the same bits."""
+    rng = np.random.default_rng(sum(seq) + split_size)
+    heads, dim, page = 1, 512, 64
+    batch = len(seq)
+    max_pages = (max(seq) + page - 1) // page
+    cfg = cache_config(1, batch, page, max_pages, heads, dim, 0)
+    pt = fill_page_table(cfg, seq)
+    for h in holes:
+        pt[h] = -1
+    n_rows = batch * max_pages * page
+    kf = rng.standard_normal((n_rows, heads, dim), dtype=np.float32)
+    if outliers:
+        hot = rng.choice(n_rows, size=n_rows // 100, replace=False)
+        kf[hot] *= 8.0
+    ck0 = oracle.f32_to_bf16(kf)
+    cv0 = randn_bf16(rng, (n_rows, heads, dim))
+    q = randn_bf16(rng, (batch, 16, dim))
+    k_new = randn_bf16(rng, (batch, heads, dim))
+    v_new = randn_bf16(rng, (batch, heads, dim))
+    pos = [n - 1 for n in seq]
+    scale = 1 / math.sqrt(dim)
+    exp_k, exp_v = ck0.copy(), cv0.copy()
+    oracle.kv_cache_write(exp_k, exp_v, cfg, pt, list(range(batch)), pos, 0, k_new, v_new)
+    exp = oracle.decode_attention(q, exp_k, exp_v, pt, seq, cfg, 0, scale)
+    ck, cv = to_dev(ck0, dev), to_dev(cv0, dev)
+    got = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, scale, split_size, num_splits,
+                      fused=(pos, k_new, v_new))
+    assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
+    assert np.array_equal(from_dev_bf16(cv).reshape(exp_v.shape), exp_v)
+    assert_close(got, exp, "1x512 fused")
+    unfused = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, scale, split_size, num_splits)
+    assert np.array_equal(unfused, got)
+
+
 def test_split_count_invariance_closed_forms(dev):
     import torch
     rng = np.random.default_rng(99)
