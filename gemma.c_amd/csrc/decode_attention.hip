@@ -24,6 +24,7 @@
 // stored split maxima are converted back to the reference's natural-log units.
 #include "gemma4_device.hpp"
 #include "decode_common.hpp"
+#include "lds_copy.hpp"
 #include "prep_common.hpp"
 
 #include "gemma4_flash_attention.h"
@@ -47,7 +48,8 @@ namespace {
 constexpr int kMaxWaves = 4;
 
 
-template <int kHeads, int kDim, int kHeadsPerWave, int kLoads, int kChunkTiles>
+template <int kHeads, int kDim, int kHeadsPerWave, int kLoads, int kChunkTiles,
+          int kWaves = kMaxWaves>
 struct DecodeShape {
   static constexpr int G = kQueryHeads / kHeads;          // GQA group
   static constexpr int GW = kHeadsPerWave;                // heads per wave
@@ -64,6 +66,10 @@ struct DecodeShape {
   // Rotary dims of the geometry: all of a sliding head, a quarter of a
   // global one (src/gemma4.h rotary settings).
   static constexpr int kRot = kHeads == 1 ? kDim / 4 : kDim;
+  static constexpr int kMaxW = kWaves;  // waves of a split workgroup at most
+  // Staged shapes: two waves per head group take alternate 8-key tiles that
+  // the workgroup copies into LDS once (all heads read every key).
+  static constexpr bool kStaged = kWaves == 2 * HG;
   static_assert(G % GW == 0, "heads per wave must divide the GQA group");
   static_assert(NP <= LPR, "one reduced score per lane at most");
   static_assert((NP & (NP - 1)) == 0 && (GW & (GW - 1)) == 0, "powers of two");
@@ -194,15 +200,15 @@ __device__ __forceinline__ uint4 prep_pack(uint4 raw, const uint16_t *weight,
 }
 
 template <class Sh>
-__global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeParams p) {
+__global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeParams p) {
   constexpr int G = Sh::G, GW = Sh::GW, HG = Sh::HG, LPR = Sh::LPR, RPL = Sh::RPL;
   constexpr int LOADS = Sh::LOADS, KT = Sh::KT, NP = Sh::NP, S = Sh::S;
   constexpr int D = LPR * kPackElems;
 
-  __shared__ int32_t s_rows[kMaxWaves][2][kWave];
-  __shared__ float s_prob[kMaxWaves][kWave];
-  __shared__ float s_ml[kMaxWaves][2][GW];
-  __shared__ float s_acc[kMaxWaves][GW][D];
+  __shared__ int32_t s_rows[Sh::kMaxW][2][kWave];
+  __shared__ float s_prob[Sh::kMaxW][kWave];
+  __shared__ float s_ml[Sh::kMaxW][2][GW];
+  __shared__ __attribute__((aligned(16))) float s_acc[Sh::kMaxW][GW][D];
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = wave_uniform(threadIdx.x / kWave);  // scalar: wave-uniform control flow
@@ -503,13 +509,87 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
     }
   };
 
+  if constexpr (Sh::kStaged) {
+    // Every head group (the 1 x 512 geometry: four groups of four heads)
+    // attends to every key of the split, so each 16-key step (two 8-key
+    // tiles, one per key lane) is copied into LDS once per workgroup -- wave
+    // w copies the K and V rows of keys 2w, 2w + 1 with global_load_lds, or
+    // zeros for an unreadable key -- and the waves read it from there: two
+    // waves per SIMD, one tile each. Two stages, one barrier per step: at
+    // step i a wave waits for its own copies of step i, the barrier
+    // publishes them and frees the stage of step i - 1, which then receives
+    // step i + 1. Rows of the split's keys come from a table filled once per
+    // window of kWindowKeys keys (one page-table load per thread).
+    constexpr int kStages = 2;
+    constexpr int kLanes = Sh::kMaxW / HG;          // key lanes: tiles per step
+    constexpr int kStepKeys = kLanes * KT;
+    constexpr int kWindowKeys = Sh::kMaxW * kWave;
+    static_assert(RPL == 1 && KT == LOADS && kStepKeys == 2 * Sh::kMaxW,
+                  "one row per load; two rows per wave per step");
+    __shared__ __attribute__((aligned(1024))) uint4 s_kv[kStages][2][kStepKeys * LPR];
+    __shared__ int32_t s_keyrow[kWindowKeys];
+    const uint32_t kv_lds = wave_uniform(lds_address(&s_kv[0][0][0]));
+    constexpr uint32_t kRowBytesKV = D * 2;
+    constexpr uint32_t kHalfBytes = kStepKeys * kRowBytesKV;  // K (or V) of one stage
+    const uint64_t kcache = reinterpret_cast<uint64_t>(p.cache_k + (int64_t)head * D);
+    const uint64_t vcache = reinterpret_cast<uint64_t>(p.cache_v + (int64_t)head * D);
+    const uint64_t knew = reinterpret_cast<uint64_t>(p.new_k + ((int64_t)b * c.num_heads + head) * D);
+    const uint64_t vnew = reinterpret_cast<uint64_t>(p.new_v + ((int64_t)b * c.num_heads + head) * D);
+    const uint32_t lane_off = (uint32_t)lane * 16;
+    auto copy_step = [&](int32_t step, int stage) __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int kk = 2 * wave + i;
+        const int32_t row = wave_uniform(s_keyrow[step * kStepKeys + kk]);
+        const uint32_t dst = stage * 2 * kHalfBytes + kk * kRowBytesKV;
+        if (row == kRowInvalid) {
+          s_kv[stage][0][kk * LPR + lane] = make_uint4(0, 0, 0, 0);
+          s_kv[stage][1][kk * LPR + lane] = make_uint4(0, 0, 0, 0);
+        } else {
+          const uint64_t off = (uint64_t)(row < 0 ? 0 : row) * Sh::kRowElems * 2;
+          const bool fresh = row == kRowNewToken;
+          copy_row_pair((fresh ? knew : kcache + off) + lane_off, kv_lds + dst);
+          copy_row_pair((fresh ? vnew : vcache + off) + lane_off, kv_lds + dst + kHalfBytes);
+        }
+      }
+    };
+    for (int32_t w0 = 0; w0 < n_keys; w0 += kWindowKeys) {
+      const int32_t wkeys = min(kWindowKeys, n_keys - w0);
+      {
+        const int32_t e = threadIdx.x;
+        const int32_t key = begin + w0 + e;
+        int32_t row = kRowInvalid;
+        if (e < wkeys) row = key == new_pos ? kRowNewToken : key_row(c, p.page_table, p.layer, b, key);
+        s_keyrow[e] = row;
+      }
+      __syncthreads();
+      const int32_t n_steps = (wkeys + kStepKeys - 1) / kStepKeys;
+      copy_step(0, 0);
+      for (int32_t i = 0; i < n_steps; ++i) {
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of step i
+        __syncthreads();
+        if (i + 1 < n_steps) copy_step(i + 1, (i + 1) % kStages);
+        const int stage = i % kStages;
+        const int32_t t0 = (i * kLanes + key_lane) * KT;  // first key of my tile
+        TileBuf tb;
+        tb.valid = 0;
+#pragma unroll
+        for (int kl = 0; kl < LOADS; ++kl) {
+          tb.valid |= (s_keyrow[t0 + kl] != kRowInvalid ? 1u : 0u) << kl;
+          tb.k[kl] = s_kv[stage][0][(key_lane * KT + kl) * LPR + cpack];
+          tb.v[kl] = s_kv[stage][1][(key_lane * KT + kl) * LPR + cpack];
+        }
+        compute(tb);
+      }
+      __syncthreads();  // the table and the stages are free for the next window
+    }
+  } else if (my_tiles > 0) {
   // Software pipeline over my chunks, CT tiles each, fully unrolled inside a
   // chunk so both register buffers are static: tile t+1's loads are in flight
   // while tile t computes, and the next chunk's page-table loads are in
   // flight for a whole chunk. Every load is issued on every path, so the
   // memory wait counters stay exact.
   static_assert(CT % 2 == 0, "tiles per chunk alternate between two buffers");
-  if (my_tiles > 0) {
     publish(0, page_row(0, fetch_page(0)));
     int32_t next_page = fetch_page(1);
     TileBuf buf0, buf1;
@@ -550,10 +630,13 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
       }
     }
     if (r == 0) {
+      // Two 16-byte stores per head (scalar stores at this 32-byte lane
+      // stride would hit the same bank eight lanes at a time).
 #pragma unroll
       for (int g = 0; g < GW; ++g) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) s_acc[wave][g][cpack * 8 + j] = acc[g][j];
+        float4 *dst = reinterpret_cast<float4 *>(&s_acc[wave][g][cpack * 8]);
+        dst[0] = make_float4(acc[g][0], acc[g][1], acc[g][2], acc[g][3]);
+        dst[1] = make_float4(acc[g][4], acc[g][5], acc[g][6], acc[g][7]);
       }
     }
     __syncthreads();
@@ -569,8 +652,16 @@ __global__ __launch_bounds__(kMaxWaves * kWave) void decode_split_kernel(DecodeP
           const int w = k * HG + hg;
           const float f = __builtin_amdgcn_exp2f(s_ml[w][0][g] - m_ref);
           big_l = fmaf(s_ml[w][1][g], f, big_l);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) sum[j] = fmaf(s_acc[w][g][cpack * 8 + j], f, sum[j]);
+          const float4 *src = reinterpret_cast<const float4 *>(&s_acc[w][g][cpack * 8]);
+          const float4 a0 = src[0], a1 = src[1];
+          sum[0] = fmaf(a0.x, f, sum[0]);
+          sum[1] = fmaf(a0.y, f, sum[1]);
+          sum[2] = fmaf(a0.z, f, sum[2]);
+          sum[3] = fmaf(a0.w, f, sum[3]);
+          sum[4] = fmaf(a1.x, f, sum[4]);
+          sum[5] = fmaf(a1.y, f, sum[5]);
+          sum[6] = fmaf(a1.z, f, sum[6]);
+          sum[7] = fmaf(a1.w, f, sum[7]);
         }
         m[g] = big_m;
         l_head[g] = big_l;
@@ -737,7 +828,7 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
 // (8 kv heads x 256): 2 GQA heads per wave, 8 loads -> 16-key tiles.
 using SlidingShape = DecodeShape<8, 256, 2, 8, 2>;
 // (1 kv head x 512): 16 GQA heads as 4 groups of 4, 8 loads -> 8-key tiles.
-using GlobalRefShape = DecodeShape<1, 512, 4, 8, 4>;
+using GlobalRefShape = DecodeShape<1, 512, 4, 8, 4, 8>;
 
 bool valid_decode_config(const Gemma4KvCacheConfig &c, int32_t layer) {
   const int64_t capacity = (int64_t)c.max_pages_per_seq * c.page_size;
@@ -751,7 +842,8 @@ template <class Sh>
 int waves_for(int32_t split_size) {
   const int chunks = (split_size + Sh::CT * Sh::KT - 1) / (Sh::CT * Sh::KT);
   int key_lanes = 1;
-  while (key_lanes * 2 * Sh::HG <= kMaxWaves && key_lanes < chunks) key_lanes *= 2;
+  if constexpr (Sh::kStaged) return Sh::kMaxW;  // two key lanes per head group, always
+  while (key_lanes * 2 * Sh::HG <= Sh::kMaxW && key_lanes < chunks) key_lanes *= 2;
   return key_lanes * Sh::HG;
 }
 
