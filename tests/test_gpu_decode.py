@@ -170,6 +170,7 @@ D512_EDGES = [
     ([4100], 512, 9, (5, 17, 30), False),   # unmapped pages inside splits
     ([8192], 128, 64, (), True),            # 1% of keys x8: the running maximum moves
     ([17], 16, 2, (), False),               # a split of one key
+    ([3000], 1024, 3, (40,), False),        # splits longer than one 512-key row window
 ]
 
 
