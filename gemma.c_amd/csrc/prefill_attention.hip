@@ -116,8 +116,11 @@ typedef unsigned u32x4v_t __attribute__((ext_vector_type(4)));
 // that all are in flight before the first MFMA; the fragments land in AGPRs.
 // k_addr is the LDS byte address of k-step 0 for this lane; k-step s sits at
 // k_addr ^ (s << 5) (the XOR swizzle of the K rows, see the kernel comment),
-// plus kImm for the stage and block. The reads are invisible to the
-// compiler's counters: fragment s is consumed only after kfrag_ready(s).
+// plus kImm for the stage and block. The swizzle changes chunk bits 0..3
+// only, so k-step s + 8 sits 256 bytes after k-step s: the reads go out in
+// pairs (s, s + 8) from one XORed address, in issue order 0, 8, 1, 9, ...
+// (kFragOrder). The reads are invisible to the compiler's counters: fragment
+// s is consumed only after kfrag_ready(s).
 template <int kImm>
 __device__ __forceinline__ void read_kfrags(uint32_t k_addr, u32x4v_t (&kf)[16]) {
   uint32_t t0, t1;
@@ -125,50 +128,48 @@ __device__ __forceinline__ void read_kfrags(uint32_t k_addr, u32x4v_t (&kf)[16])
       "s_waitcnt lgkmcnt(0)\n\t"
       "v_xor_b32 %[t0], 0, %[ka]\n\t"
       "ds_read_b128 %[f0], %[t0] offset:%[imm]\n\t"
+      "ds_read_b128 %[f8], %[t0] offset:%[imm2]\n\t"
       "v_xor_b32 %[t1], 32, %[ka]\n\t"
       "ds_read_b128 %[f1], %[t1] offset:%[imm]\n\t"
+      "ds_read_b128 %[f9], %[t1] offset:%[imm2]\n\t"
       "v_xor_b32 %[t0], 64, %[ka]\n\t"
       "ds_read_b128 %[f2], %[t0] offset:%[imm]\n\t"
+      "ds_read_b128 %[f10], %[t0] offset:%[imm2]\n\t"
       "v_xor_b32 %[t1], 96, %[ka]\n\t"
       "ds_read_b128 %[f3], %[t1] offset:%[imm]\n\t"
+      "ds_read_b128 %[f11], %[t1] offset:%[imm2]\n\t"
       "v_xor_b32 %[t0], 128, %[ka]\n\t"
       "ds_read_b128 %[f4], %[t0] offset:%[imm]\n\t"
+      "ds_read_b128 %[f12], %[t0] offset:%[imm2]\n\t"
       "v_xor_b32 %[t1], 160, %[ka]\n\t"
       "ds_read_b128 %[f5], %[t1] offset:%[imm]\n\t"
+      "ds_read_b128 %[f13], %[t1] offset:%[imm2]\n\t"
       "v_xor_b32 %[t0], 192, %[ka]\n\t"
       "ds_read_b128 %[f6], %[t0] offset:%[imm]\n\t"
+      "ds_read_b128 %[f14], %[t0] offset:%[imm2]\n\t"
       "v_xor_b32 %[t1], 224, %[ka]\n\t"
       "ds_read_b128 %[f7], %[t1] offset:%[imm]\n\t"
-      "v_xor_b32 %[t0], 256, %[ka]\n\t"
-      "ds_read_b128 %[f8], %[t0] offset:%[imm]\n\t"
-      "v_xor_b32 %[t1], 288, %[ka]\n\t"
-      "ds_read_b128 %[f9], %[t1] offset:%[imm]\n\t"
-      "v_xor_b32 %[t0], 320, %[ka]\n\t"
-      "ds_read_b128 %[f10], %[t0] offset:%[imm]\n\t"
-      "v_xor_b32 %[t1], 352, %[ka]\n\t"
-      "ds_read_b128 %[f11], %[t1] offset:%[imm]\n\t"
-      "v_xor_b32 %[t0], 384, %[ka]\n\t"
-      "ds_read_b128 %[f12], %[t0] offset:%[imm]\n\t"
-      "v_xor_b32 %[t1], 416, %[ka]\n\t"
-      "ds_read_b128 %[f13], %[t1] offset:%[imm]\n\t"
-      "v_xor_b32 %[t0], 448, %[ka]\n\t"
-      "ds_read_b128 %[f14], %[t0] offset:%[imm]\n\t"
-      "v_xor_b32 %[t1], 480, %[ka]\n\t"
-      "ds_read_b128 %[f15], %[t1] offset:%[imm]"
+      "ds_read_b128 %[f15], %[t1] offset:%[imm2]"
       : [t0] "=&v"(t0), [t1] "=&v"(t1),
         [f0] "=&a"(kf[0]), [f1] "=&a"(kf[1]), [f2] "=&a"(kf[2]), [f3] "=&a"(kf[3]), [f4]
         "=&a"(kf[4]), [f5] "=&a"(kf[5]), [f6] "=&a"(kf[6]), [f7] "=&a"(kf[7]), [f8]
         "=&a"(kf[8]), [f9] "=&a"(kf[9]), [f10] "=&a"(kf[10]), [f11] "=&a"(kf[11]), [f12]
         "=&a"(kf[12]), [f13] "=&a"(kf[13]), [f14] "=&a"(kf[14]), [f15] "=&a"(kf[15])
-      : [ka] "v"(k_addr), [imm] "i"(kImm));
+      : [ka] "v"(k_addr), [imm] "i"(kImm), [imm2] "i"(kImm + 256));
 }
 
+// Issue position p of read_kfrags reads k-step kFragOrder(p).
+constexpr int kFragOrder(int p) { return (p >> 1) + 8 * (p & 1); }
+// Issue position of k-step s.
+constexpr int kFragPos(int s) { return s < 8 ? 2 * s : 2 * (s - 8) + 1; }
+
 // Waits until fragment kStep of read_kfrags has landed (LDS returns in
-// order, so at most 15 - kStep of the block's reads may still be pending;
-// any other LDS or scalar load in flight only makes the wait stricter).
+// order, so at most 15 - kFragPos(kStep) of the block's reads may still be
+// pending; any other LDS or scalar load in flight only makes the wait
+// stricter).
 template <int kStep>
 __device__ __forceinline__ void kfrag_ready(u32x4v_t &f) {
-  asm volatile("s_waitcnt lgkmcnt(%[n])" : "+a"(f) : [n] "i"(15 - kStep));
+  asm volatile("s_waitcnt lgkmcnt(%[n])" : "+a"(f) : [n] "i"(15 - kFragPos(kStep)));
 }
 
 // f(integral_constant<int, I>) for I = kBegin .. kEnd-1, unrolled.
@@ -408,18 +409,20 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     u32x4v_t kf[KS];
     read_kfrags<kImm>(k_addr, kf);
     f32x16_t s_acc = f32x16_t{};
-    auto step_s = [&](auto sc) __attribute__((always_inline)) {
-      constexpr int s = decltype(sc)::value;
+    // The k-steps in the order their fragments arrive (kFragOrder).
+    auto step_s = [&](auto pc) __attribute__((always_inline)) {
+      constexpr int pos = decltype(pc)::value;
+      constexpr int s = kFragOrder(pos);
       kfrag_ready<s>(kf[s]);
       s_acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf[s]),
                                                       __builtin_bit_cast(bf16x8_t, qreg[s]), s_acc,
                                                       0, 0, 0);
       if constexpr (kBlk == 1) {
         if (copy) {
-          if constexpr (s % 2 == 0) {
-            copy_row_pair(ksrc[s / 2], k_dst[S ^ 1] + (s / 2) * 2 * kRowBytes);
+          if constexpr (pos % 2 == 0) {
+            copy_row_pair(ksrc[pos / 2], k_dst[S ^ 1] + (pos / 2) * 2 * kRowBytes);
           } else {
-            copy_row_pair(vsrc[s / 2], v_dst[S ^ 1] + (s / 2) * 2 * kRowBytes);
+            copy_row_pair(vsrc[pos / 2], v_dst[S ^ 1] + (pos / 2) * 2 * kRowBytes);
           }
         }
       }
