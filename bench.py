@@ -301,8 +301,15 @@ def bench_prefill(torch, gk, dev, reps):
         out = torch.zeros((1, lq, QH, DIM), dtype=torch.int16, device=dev)
         pr = torch.tensor([prior], dtype=torch.int32, device=dev)
 
-        raw = gk.lib().gemma4_flash_attention_prefill_chunk_paged_bf16
         args = [gk.ptr(t) for t in (out, q, k, v, ck, cv, pt, pr)] + [cfg, 0, 1, lq, 1 / 16]
+        if window or os.environ.get("GEMMA_KV_PREFILL_PLAIN"):
+            raw = gk.lib().gemma4_flash_attention_prefill_chunk_paged_bf16
+        else:
+            # The global chunk's causal work balanced over workgroups.
+            nbytes = gk.flash_attention_prefill_chunk_workspace_bytes(1, lq, cfg)
+            ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+            raw = gk.lib().gemma4_flash_attention_prefill_chunk_paged_bf16_ws
+            args += [gk.ptr(ws), nbytes]
 
         def fn(st):
             code = raw(*args, st)

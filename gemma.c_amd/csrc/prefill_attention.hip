@@ -88,7 +88,16 @@ struct PrefillParams {
   int32_t chunk_len;
   int32_t window;            // 0: global (causal only)
   float q_scale;             // softmax_scale * log2(e)
+  // Balanced global chunks (n_pairs > 0): row blocks j and nb-1-j form a
+  // pair served by two workgroups with equal key work; the one row block a
+  // pair splits meets in ws_partial (per split slot, two halves of
+  // kPartialFloats x 256 floats) and ws_counters (arrivals, re-armed to 0).
+  int32_t n_pairs;
+  float *ws_partial;
+  int32_t *ws_counters;
 };
+
+constexpr int kPartialFloats = 130;  // per thread: 128 accumulators, max, sum
 
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -184,6 +193,7 @@ __device__ __forceinline__ void static_for(F &&f) {
 template <int kSt>
 using Stage = std::integral_constant<int, kSt>;
 
+template <bool kPaired>
 __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(PrefillParams p) {
   constexpr int KS = kDim / 16;        // k-steps of S^T (dims)
   constexpr int DB = kDim / 32;        // 32-dim blocks of O^T
@@ -215,10 +225,55 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int n = lane & 31;          // MFMA column = query row of this lane
   const int Hk = p.c.num_heads;
   const int head = blockIdx.x % Hk;
-  const int q0 = (blockIdx.x / Hk) * kPrefillRows;
   const int b = blockIdx.y;
   const int Lq = p.chunk_len;
   const int prior = p.prior != nullptr ? wave_uniform(p.prior[b]) : 0;
+
+  // ---- work units: (row block, tile range, split slot) -------------------
+  // Plain: one row block per workgroup. Balanced (global chunks): row
+  // blocks j and J = nb-1-j need T(j) + T(J) key tiles together; workgroup
+  // A takes block j and the first x tiles of block J, workgroup B the other
+  // T(J) - x, with x chosen so both get half. A split block's two halves
+  // merge through the workspace.
+  struct Unit {
+    int q0, t_lo, t_hi, slot, part;
+  };
+  Unit units[2];
+  int n_units = 0;
+  constexpr int kAllTiles = 1 << 30;
+  if constexpr (kPaired) {
+    const int rest = blockIdx.x / Hk;
+    const int pair = rest >> 1, side = rest & 1;
+    const int nb = (Lq + kPrefillRows - 1) / kPrefillRows;
+    const int j = pair, J = nb - 1 - pair;
+    auto tiles_of = [&](int blk) {  // causal, no window: tiles 0 .. last key
+      return (prior + min(kPrefillRows * (blk + 1), Lq) - 1) / kTileKeys + 1;
+    };
+    if (j == J) {
+      if (side == 0) units[n_units++] = {kPrefillRows * j, 0, kAllTiles, -1, 0};
+    } else if (j < J) {
+      const int tj = tiles_of(j), tJ = tiles_of(J);
+      int x = (tj + tJ) / 2 - tj;
+      x = x < 0 ? 0 : (x > tJ ? tJ : x);
+      const int slot = (b * Hk + head) * p.n_pairs + pair;
+      if (side == 0) {
+        units[n_units++] = {kPrefillRows * j, 0, kAllTiles, -1, 0};
+        if (x > 0) units[n_units++] = {kPrefillRows * J, 0, x, x < tJ ? slot : -1, 0};
+      } else if (x < tJ) {
+        units[n_units++] = {kPrefillRows * J, x, kAllTiles, x > 0 ? slot : -1, 1};
+      }
+    }
+  } else {
+    units[n_units++] = {(int)(blockIdx.x / Hk) * kPrefillRows, 0, kAllTiles, -1, 0};
+  }
+  __shared__ int s_last;
+
+  for (int u = 0; u < n_units; ++u) {
+  const int q0 = wave_uniform(units[u].q0);
+  const int unit_lo = wave_uniform(units[u].t_lo);
+  const int unit_hi = wave_uniform(units[u].t_hi);
+  const int unit_slot = wave_uniform(units[u].slot);
+  const int unit_part = wave_uniform(units[u].part);
 
   // Rows of this lane: chunk row r = q0 + 16*wave + n % 16, q head 2*head + n / 16
   // (G = 2 for 16 query heads over 8 kv heads).
@@ -252,8 +307,11 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   const int wg_last = prior + min(q0 + kPrefillRows, Lq) - 1;  // last visible key of any row
   int kstart = p.window > 0 ? prior + q0 - p.window + 1 : 0;
   kstart = kstart < 0 ? 0 : kstart;
-  const int tile0 = (kstart / kTileKeys) * kTileKeys;
-  const int n_tiles = (wg_last - tile0) / kTileKeys + 1;
+  const int tile0_rows = (kstart / kTileKeys) * kTileKeys;
+  const int n_tiles_rows = (wg_last - tile0_rows) / kTileKeys + 1;
+  // This unit's tiles of the row block.
+  const int tile0 = tile0_rows + unit_lo * kTileKeys;
+  const int n_tiles = min(n_tiles_rows, unit_hi) - unit_lo;
 
   // ---- key rows: page lookup one tile ahead, addresses at copy time ------
   // Lane j (= lane % 16) of wave w resolves key tile + 16w + j.
@@ -549,23 +607,80 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     step(Stage<0>{}, it);
     if (it + 1 < n_tiles) step(Stage<1>{}, it + 1);
   }
-  wait_copies();  // no copy may still be writing LDS when the workgroup exits
+  wait_copies();  // no copy may still be writing LDS when the unit ends
 
-  // Normalise and store: lane holds dims 32d + (i/4)*8 + 4*half + i%4 of row n.
-  l_run += lane_xor<32>(l_run);
-  if (!row_ok) return;
-  const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-  uint16_t *orow = p.out + (((int64_t)b * Lq + row) * kQueryHeads + qh) * kDim;
+  // A split row block: store this half's partial (device-coherent: the
+  // other half may run on another XCD), count the arrival, and let the
+  // second arriver merge both halves and write the rows.
+  bool emit = true;
+  if (unit_slot >= 0) {
+    float *mine = p.ws_partial + ((int64_t)unit_slot * 2 + unit_part) * kPartialFloats * kPrefillThreads;
+    const float *other =
+        p.ws_partial + ((int64_t)unit_slot * 2 + (unit_part ^ 1)) * kPartialFloats * kPrefillThreads;
 #pragma unroll
-  for (int d = 0; d < DB; ++d) {
+    for (int d = 0; d < DB; ++d) {
 #pragma unroll
-    for (int i = 0; i < 16; i += 4) {
-      uint2 o;
-      o.x = pack_bf16x2(acc[d][i] * inv, acc[d][i + 1] * inv);
-      o.y = pack_bf16x2(acc[d][i + 2] * inv, acc[d][i + 3] * inv);
-      *reinterpret_cast<uint2 *>(orow + 32 * d + (i / 4) * 8 + 4 * half) = o;
+      for (int i = 0; i < 16; ++i)
+        __hip_atomic_store(mine + (d * 16 + i) * kPrefillThreads + t, acc[d][i], __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __hip_atomic_store(mine + 128 * kPrefillThreads + t, m_run, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(mine + 129 * kPrefillThreads + t, l_run, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
+    __syncthreads();
+    if (t == 0) {
+      int32_t *counter = p.ws_counters + unit_slot;
+      const int32_t arrived =
+          __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (arrived == 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = arrived == 1 ? 1 : 0;
+    }
+    __syncthreads();
+    emit = s_last != 0;
+    if (emit) {
+      const float mo = __hip_atomic_load(other + 128 * kPrefillThreads + t, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+      const float lo = __hip_atomic_load(other + 129 * kPrefillThreads + t, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+      const float mm = fmaxf(m_run, mo);
+      const float fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - mm);
+      const float fb = mo == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mo - mm);
+      l_run = l_run * fa + lo * fb;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float ao = __hip_atomic_load(other + (d * 16 + i) * kPrefillThreads + t,
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          acc[d][i] = acc[d][i] * fa + ao * fb;
+        }
+      }
+      m_run = mm;
     }
   }
+
+  if (emit) {
+    // Normalise and store: lane holds dims 32d + (i/4)*8 + 4*half + i%4 of row n.
+    l_run += lane_xor<32>(l_run);
+    if (row_ok) {
+      const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+      uint16_t *orow = p.out + (((int64_t)b * Lq + row) * kQueryHeads + qh) * kDim;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 4) {
+          uint2 o;
+          o.x = pack_bf16x2(acc[d][i] * inv, acc[d][i + 1] * inv);
+          o.y = pack_bf16x2(acc[d][i + 2] * inv, acc[d][i + 3] * inv);
+          *reinterpret_cast<uint2 *>(orow + 32 * d + (i / 4) * 8 + 4 * half) = o;
+        }
+      }
+    }
+  }
+  if constexpr (kPaired) __syncthreads();  // the next unit reuses the LDS stages and tables
+  }  // units
 }
 
 }  // namespace
@@ -573,12 +688,30 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
 
 using namespace gemma4;
 
-extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
-    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
-    const gemma4_bf16 *d_v, const gemma4_bf16 *d_cache_k, const gemma4_bf16 *d_cache_v,
-    const int32_t *d_page_table, const int32_t *d_prior_lengths, Gemma4KvCacheConfig config,
-    int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
-    hipStream_t stream) {
+namespace {
+
+// Balanced-mode geometry of a chunk: row-block pairs per (sequence, head) and
+// the workspace bytes: arrival counters (256-byte aligned), then two partial
+// halves per split slot.
+int prefill_pairs(int32_t chunk_len) {
+  const int nb = (chunk_len + kPrefillRows - 1) / kPrefillRows;
+  return nb < 2 ? 0 : (nb + 1) / 2;
+}
+size_t prefill_counter_bytes(int64_t slots) { return (size_t)((slots * 4 + 255) / 256 * 256); }
+size_t prefill_workspace_bytes(int32_t batch_size, int32_t chunk_len, int32_t heads) {
+  if (batch_size <= 0 || chunk_len <= 0 || heads <= 0) return 0;
+  const int64_t slots = (int64_t)batch_size * heads * prefill_pairs(chunk_len);
+  if (slots == 0) return 0;
+  return prefill_counter_bytes(slots) + (size_t)slots * 2 * kPartialFloats * kPrefillThreads * 4;
+}
+
+hipError_t prefill_chunk_launch(gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+                                const gemma4_bf16 *d_v, const gemma4_bf16 *d_cache_k,
+                                const gemma4_bf16 *d_cache_v, const int32_t *d_page_table,
+                                const int32_t *d_prior_lengths, Gemma4KvCacheConfig config,
+                                int32_t layer, int32_t batch_size, int32_t chunk_len,
+                                float softmax_scale, void *d_workspace, size_t workspace_bytes,
+                                bool balanced, hipStream_t stream) {
   if (batch_size == 0 || chunk_len == 0) return hipSuccess;
   const bool paged = d_prior_lengths != nullptr;
   if (batch_size < 0 || chunk_len < 0 || batch_size > 65535 || !(softmax_scale > 0.0f) ||
@@ -590,6 +723,11 @@ extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
                 layer < 0 || layer >= config.num_layers || config.page_size <= 0 ||
                 config.max_pages_per_seq <= 0 || config.num_pages <= 0 ||
                 batch_size > config.batch_size)) {
+    return hipErrorInvalidValue;
+  }
+  const size_t need = prefill_workspace_bytes(batch_size, chunk_len, config.num_heads);
+  if (balanced && (d_workspace == nullptr || workspace_bytes < need ||
+                   (reinterpret_cast<uintptr_t>(d_workspace) & 255) != 0)) {
     return hipErrorInvalidValue;
   }
   PrefillParams p;
@@ -611,8 +749,56 @@ extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
   p.chunk_len = chunk_len;
   p.window = config.window_size;
   p.q_scale = softmax_scale * kLog2e;
-  const int blocks = config.num_heads * ((chunk_len + kPrefillRows - 1) / kPrefillRows);
-  hipLaunchKernelGGL(prefill_chunk_kernel, dim3(blocks, batch_size), dim3(kPrefillThreads), 0,
-                     stream, p);
+  // Sliding chunks already carry equal work per row block; only causal
+  // (global) chunks of two or more row blocks are paired.
+  p.n_pairs = balanced && config.window_size == 0 ? prefill_pairs(chunk_len) : 0;
+  p.ws_counters = nullptr;
+  p.ws_partial = nullptr;
+  int blocks = config.num_heads * ((chunk_len + kPrefillRows - 1) / kPrefillRows);
+  if (p.n_pairs > 0) {
+    const int64_t slots = (int64_t)batch_size * config.num_heads * p.n_pairs;
+    p.ws_counters = static_cast<int32_t *>(d_workspace);
+    p.ws_partial = reinterpret_cast<float *>(static_cast<char *>(d_workspace) +
+                                             prefill_counter_bytes(slots));
+    blocks = config.num_heads * 2 * p.n_pairs;
+  }
+  if (p.n_pairs > 0) {
+    hipLaunchKernelGGL(prefill_chunk_kernel<true>, dim3(blocks, batch_size),
+                       dim3(kPrefillThreads), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL(prefill_chunk_kernel<false>, dim3(blocks, batch_size),
+                       dim3(kPrefillThreads), 0, stream, p);
+  }
   return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
+    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_v, const gemma4_bf16 *d_cache_k, const gemma4_bf16 *d_cache_v,
+    const int32_t *d_page_table, const int32_t *d_prior_lengths, Gemma4KvCacheConfig config,
+    int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
+    hipStream_t stream) {
+  return prefill_chunk_launch(d_out, d_q, d_k, d_v, d_cache_k, d_cache_v, d_page_table,
+                              d_prior_lengths, config, layer, batch_size, chunk_len,
+                              softmax_scale, nullptr, 0, false, stream);
+}
+
+extern "C" size_t gemma4_flash_attention_prefill_chunk_workspace_bytes(
+    int32_t batch_size, int32_t chunk_len, Gemma4KvCacheConfig config) {
+  return config.window_size == 0 ? prefill_workspace_bytes(batch_size, chunk_len, config.num_heads)
+                                 : 0;
+}
+
+extern "C" hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16_ws(
+    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_v, const gemma4_bf16 *d_cache_k, const gemma4_bf16 *d_cache_v,
+    const int32_t *d_page_table, const int32_t *d_prior_lengths, Gemma4KvCacheConfig config,
+    int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
+    void *d_workspace, size_t workspace_bytes, hipStream_t stream) {
+  const bool balanced = config.window_size == 0 && prefill_pairs(chunk_len) > 0;
+  return prefill_chunk_launch(d_out, d_q, d_k, d_v, d_cache_k, d_cache_v, d_page_table,
+                              d_prior_lengths, config, layer, batch_size, chunk_len,
+                              softmax_scale, d_workspace, workspace_bytes, balanced, stream);
 }

@@ -81,6 +81,9 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _P]),
     "gemma4_flash_attention_prefill_chunk_paged_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _F32, _P]),
+    "gemma4_flash_attention_prefill_chunk_workspace_bytes": (ctypes.c_size_t, [_I32, _I32, _CFG]),
+    "gemma4_flash_attention_prefill_chunk_paged_bf16_ws": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _I32, _I32, _F32, _P, ctypes.c_size_t, _P]),
     "gemma4_flash_attention_sliding_fwd_bf16_norm_rope": (
         _I32, [_P] * 12 + [_I32, _I32, _I32, _I32, _F32, _P]),
     "gemma4_flash_attention_global_fwd_bf16_norm_rope": (
@@ -448,6 +451,20 @@ def attention_o_projection_post_norm_bf16(residual_out, normed_out, ffn_residual
         ptr(residual_out), ptr(normed_out), ptr(ffn_residual), ptr(attention_out),
         ptr(o_proj_col_major), ptr(post_norm_weight), ptr(attention_x), rows, attention_width,
         stream_handle(stream))
+
+
+def flash_attention_prefill_chunk_workspace_bytes(batch_size, chunk_len, config) -> int:
+    return lib().gemma4_flash_attention_prefill_chunk_workspace_bytes(batch_size, chunk_len, config)
+
+
+def flash_attention_prefill_chunk_paged_bf16_ws(out, q, k, v, cache_k, cache_v, page_table,
+                                                prior_lengths, config, layer, batch_size,
+                                                chunk_len, softmax_scale, workspace,
+                                                workspace_bytes, stream=None) -> int:
+    return lib().gemma4_flash_attention_prefill_chunk_paged_bf16_ws(
+        ptr(out), ptr(q), ptr(k), ptr(v), ptr(cache_k), ptr(cache_v), ptr(page_table),
+        ptr(prior_lengths), config, layer, batch_size, chunk_len, softmax_scale, ptr(workspace),
+        workspace_bytes, stream_handle(stream))
 
 
 def flash_attention_prefill_chunk_paged_bf16(out, q, k, v, cache_k, cache_v, page_table,

@@ -154,6 +154,27 @@ hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
     int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
     hipStream_t stream);
 
+// The same attention with the causal work of a global chunk (window 0, two
+// or more 64-row blocks) balanced over workgroups: row blocks j and nb-1-j
+// are served by two workgroups with equal key tiles, and the one block a pair
+// splits is merged through d_workspace. Results equal the entry point above
+// up to float summation order. d_workspace: at least
+// gemma4_flash_attention_prefill_chunk_workspace_bytes(batch_size,
+// chunk_len, config) bytes, 256-byte aligned, zero-filled once before its
+// first use (every call leaves its arrival counters at zero again); calls
+// that share a workspace must not overlap. Sliding chunks (window > 0) run
+// the plain kernel and ignore the workspace. No counterpart in the
+// reference, whose prefill launcher (src/gemma4_flash_attention_prefill.cu:
+// 1131-1183) assigns one causal row block per block.
+size_t gemma4_flash_attention_prefill_chunk_workspace_bytes(
+    int32_t batch_size, int32_t chunk_len, Gemma4KvCacheConfig config);
+hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16_ws(
+    gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
+    const gemma4_bf16 *d_v, const gemma4_bf16 *d_cache_k, const gemma4_bf16 *d_cache_v,
+    const int32_t *d_page_table, const int32_t *d_prior_lengths, Gemma4KvCacheConfig config,
+    int32_t layer, int32_t batch_size, int32_t chunk_len, float softmax_scale,
+    void *d_workspace, size_t workspace_bytes, hipStream_t stream);
+
 // Prefill self-attention with Q/K/V preparation (seqlen_q == seqlen_k, no
 // prior context), same names, argument order and validation as the
 // reference launchers (src/gemma4_flash_attention.cuh:9-45,

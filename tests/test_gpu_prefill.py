@@ -73,7 +73,94 @@ def test_prefill_chunk_matches_oracle(dev, window, page, priors, lq):
     assert_close(from_dev_bf16(out), exp, f"prefill window={window} priors={priors}")
 
 
-@pytest.mark.parametrize("layer_kind", ["sliding", "global"])
+def _run_balanced(dev, rng, priors, lq, page, ws=None):
+    """One global chunk through the balanced entry point and the plain one;
+    returns both outputs, the oracle's and the workspace (reused when given)."""
+    import torch
+    batch = len(priors)
+    scale = 1 / math.sqrt(D)
+    q = randn_bf16(rng, (batch, lq, 16, D))
+    k = randn_bf16(rng, (batch, lq, H, D))
+    v = randn_bf16(rng, (batch, lq, H, D))
+    max_pages = (max(priors) + page - 1) // page + 1
+    cfg = cache_config(1, batch, page, max_pages, H, D, 0)
+    pt = fill_page_table(cfg, priors)
+    ck = randn_bf16(rng, (batch * max_pages * page, H, D))
+    cv = randn_bf16(rng, (batch * max_pages * page, H, D))
+    c = gk.make_config(*cfg)
+    nbytes = gk.flash_attention_prefill_chunk_workspace_bytes(batch, lq, c)
+    if ws is None:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    assert ws.numel() >= nbytes
+    args = [to_dev(x, dev) for x in (q, k, v, ck, cv, pt, np.asarray(priors, np.int32))]
+    out_ws = empty_bf16((batch, lq, 16, D), dev)
+    out_plain = empty_bf16((batch, lq, 16, D), dev)
+    gk.check(gk.flash_attention_prefill_chunk_paged_bf16_ws(
+        out_ws, *args, c, 0, batch, lq, scale, ws, ws.numel()), "balanced")
+    gk.check(gk.flash_attention_prefill_chunk_paged_bf16(
+        out_plain, *args, c, 0, batch, lq, scale), "plain")
+    torch.cuda.synchronize()
+    exp = np.zeros((batch, lq, 16, D), np.uint16)
+    for b, pr in enumerate(priors):
+        kf = _full_keys(ck, cfg, pt, b, pr, k[b])
+        vf = _full_keys(cv, cfg, pt, b, pr, v[b])
+        exp[b] = oracle.prefill_attention(q[b:b + 1], kf[None], vf[None], lq, pr + lq, 16, H, D,
+                                          0, scale)[0]
+    return from_dev_bf16(out_ws), from_dev_bf16(out_plain), exp, ws
+
+
+@pytest.mark.parametrize("priors,lq,page", [
+    ([0], 65, 16),          # two row blocks, too close to split
+    ([0], 200, 16),         # four blocks: pairs (0, 3) split, (1, 2) not
+    ([0], 130, 16),         # three blocks: the middle one unpaired
+    ([100, 3], 321, 16),    # ragged priors, six blocks, a partial last block
+    ([0, 33], 384, 8),      # one sequence with no prior
+    ([700], 512, 64),       # prior longer than the chunk
+])
+def test_prefill_balanced_global_matches_oracle(dev, priors, lq, page):
+    """The balanced global chunk (row blocks j and nb-1-j paired, the split
+    block merged through the workspace) equals the oracle, and the plain
+    kernel's output within the same tolerance; a second call on the same
+    workspace with a smaller input checks that the arrival counters re-arm."""
+    rng = np.random.default_rng(lq + sum(priors))
+    got, plain, exp, ws = _run_balanced(dev, rng, priors, lq, page)
+    assert_close(got, exp, f"balanced priors={priors} lq={lq}")
+    assert_close(got, plain, f"balanced vs plain priors={priors} lq={lq}")
+    got2, _, exp2, _ = _run_balanced(dev, rng, priors[:1], max(lq // 2, 65), page, ws)
+    assert_close(got2, exp2, f"balanced second call priors={priors[:1]}")
+    pairs = ((lq + 63) // 64 + 1) // 2
+    counter_bytes = (len(priors) * H * pairs * 4 + 255) // 256 * 256
+    assert not ws[:counter_bytes].any().item()  # every arrival counter re-armed to zero
+
+
+def test_prefill_balanced_argument_checks(dev):
+    import torch
+    cfg = gk.make_config(*cache_config(1, 1, 16, 4, H, D, 0))
+    sliding = gk.make_config(*cache_config(1, 1, 16, 4, H, D, 32))
+    lq = 256
+    nbytes = gk.flash_attention_prefill_chunk_workspace_bytes(1, lq, cfg)
+    # Counters (256-byte block) + 2 pairs x 8 heads x 2 halves x 130 x 256 floats.
+    assert nbytes == 256 + 2 * 8 * 2 * 130 * 256 * 4
+    assert gk.flash_attention_prefill_chunk_workspace_bytes(1, lq, sliding) == 0
+    assert gk.flash_attention_prefill_chunk_workspace_bytes(1, 64, cfg) == 0  # one row block
+    x = torch.zeros((1, lq, 16, D), dtype=torch.int16, device=dev)
+    kv = torch.zeros((1, lq, H, D), dtype=torch.int16, device=dev)
+    ws = torch.zeros(nbytes + 512, dtype=torch.uint8, device=dev)
+    base = [x, x, kv, kv, None, None, None, None]
+    bad = gk.HIP_ERROR_INVALID_VALUE
+    assert gk.flash_attention_prefill_chunk_paged_bf16_ws(*base, cfg, 0, 1, lq, 0.1, None, 0) == bad
+    assert gk.flash_attention_prefill_chunk_paged_bf16_ws(
+        *base, cfg, 0, 1, lq, 0.1, ws, nbytes - 1) == bad
+    assert gk.flash_attention_prefill_chunk_paged_bf16_ws(
+        *base, cfg, 0, 1, lq, 0.1, ws.data_ptr() + 4, nbytes) == bad
+    # Sliding chunks and single row blocks need no workspace.
+    assert gk.flash_attention_prefill_chunk_paged_bf16_ws(*base, sliding, 0, 1, lq, 0.1, None, 0) == 0
+    assert gk.flash_attention_prefill_chunk_paged_bf16_ws(*base, cfg, 0, 1, 64, 0.1, None, 0) == 0
+    assert gk.flash_attention_prefill_chunk_paged_bf16_ws(*base, cfg, 0, 1, lq, 0.1, ws, nbytes) == 0
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("layer_kind", ["sliding", "global", "global_balanced"])
 def test_prefill_config5_full_size_against_torch_fp32(dev, layer_kind):
     """2048-row chunk; sliding (window 1024, page-1 ring of
     1024 slots holding the last 1024 of a 1536-token prior) or global (prior
@@ -98,10 +185,15 @@ def test_prefill_config5_full_size_against_torch_fp32(dev, layer_kind):
     q, k, v = rnd((1, lq, 16, D)), rnd((1, lq, H, D)), rnd((1, lq, H, D))
     out = empty_bf16((1, lq, 16, D), dev)
     scale = 1 / 16
-    gk.check(gk.flash_attention_prefill_chunk_paged_bf16(
-        out, q.view(torch.int16), k.view(torch.int16), v.view(torch.int16), ck.view(torch.int16),
-        cv.view(torch.int16), to_dev(pt, dev), to_dev(np.array([prior], np.int32), dev),
-        gk.make_config(*cfg), 0, 1, lq, scale))
+    args = [out, q.view(torch.int16), k.view(torch.int16), v.view(torch.int16),
+            ck.view(torch.int16), cv.view(torch.int16), to_dev(pt, dev),
+            to_dev(np.array([prior], np.int32), dev), gk.make_config(*cfg), 0, 1, lq, scale]
+    if layer_kind == "global_balanced":
+        nbytes = gk.flash_attention_prefill_chunk_workspace_bytes(1, lq, args[8])
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        gk.check(gk.flash_attention_prefill_chunk_paged_bf16_ws(*args, ws, nbytes))
+    else:
+        gk.check(gk.flash_attention_prefill_chunk_paged_bf16(*args))
     # fp32 reference: gather the visible prior keys through the ring, then the chunk.
     kpos = torch.arange(prior + lq, device=dev)
     lp = kpos // page
