@@ -19,14 +19,18 @@
 // 4 (l/16) + i, so P^T feeds the second MFMA from registers when its 32-key
 // contraction order is permuted to {4g..4g+3, 16+4g..16+4g+3} for lane
 // group g, and V^T is read in that order by two ds_read_b64_tr_b16 per
-// operand. O^T is 128 fp32 per lane, Q^T 64 registers. A workgroup is four
+// operand. O^T is 128 fp32 per lane (VGPR accumulator form, a build flag
+// for this file), Q^T 64 registers held in AGPRs. A workgroup is four
 // consecutive rows that share 32-key K/V tiles copied into two LDS stages
 // with global_load_lds (tile t+1 in flight while tile t is computed; K chunk
 // c of key k at c ^ (k & 15), V chunk c at c ^ ((k & 7) << 1), 16-byte
-// chunks, so the operand reads are bank-conflict free). The lazy online softmax of
-// the chunk kernel (maximum moved only when it grows by more than 8 in
-// log2 units). This geometry is outside the BASELINE configs; the kernel is
-// written for parity, not tuned.
+// chunks, so the operand reads are bank-conflict free). Scheduling: each
+// score block issues its 16 K-fragment reads into AGPRs before its first
+// MFMA (one counter wait per MFMA, two accumulator chains), and the P.V
+// phase keeps its transposing V reads four MFMAs ahead. The lazy online
+// softmax of the chunk kernel (maximum moved only when it grows by more than
+// 8 in log2 units). Per 32-key tile a wave reads 64 KiB of K and V from LDS
+// for 16 query columns, so the kernel is bound by LDS reads, not MFMA.
 #include "gemma4_device.hpp"
 #include "lds_copy.hpp"
 #include "prep_common.hpp"
@@ -34,6 +38,7 @@
 #include "gemma4_flash_attention.h"
 
 #include <math.h>
+#include <type_traits>
 
 namespace gemma4 {
 namespace {
@@ -122,6 +127,7 @@ constexpr int kD512Tile = 32;         // keys per LDS tile
 constexpr int kD512RowBytes = kD512 * 2;
 constexpr int kD512Chunks = kD512RowBytes / 16;  // 16-byte chunks per row
 constexpr float kD512Slack = 8.0f;
+constexpr int kD512VLead = 4;         // P.V MFMAs the V reads run ahead
 
 struct D512Params {
   uint16_t *out;        // [B][L][16][512]
@@ -135,6 +141,62 @@ struct D512Params {
 __device__ __forceinline__ f32x4_t mfma16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+typedef unsigned u32x4v_t __attribute__((ext_vector_type(4)));
+
+// The 16 K-fragment reads of one 16-key score block into AGPRs, all in
+// flight before the first MFMA. For lane key k (k & 15 = lane & 15) and lane
+// group g, k-step s sits at chunk (4s + g) ^ (k & 15) of the key's row: bits
+// 0-1 of the chunk are g ^ (k & 3), bits 2-3 are (s & 3) ^ ((k >> 2) & 3)
+// and bits 4+ are s >> 2. So with base = the address of k-step 0, k-step s
+// is at (base ^ (64 (s & 3))) + 256 (s >> 2): four XORed addresses, four
+// immediate offsets each. Issue position p = 4 (s & 3) + (s >> 2).
+template <int kImm>
+__device__ __forceinline__ void d512_read_kfrags(uint32_t k_addr, u32x4v_t (&kf)[16]) {
+  uint32_t t0, t1;
+  asm volatile(
+      "s_waitcnt lgkmcnt(0)\n\t"
+      "v_xor_b32 %[t0], 0, %[ka]\n\t"
+      "ds_read_b128 %[f0], %[t0] offset:%[i0]\n\t"
+      "ds_read_b128 %[f4], %[t0] offset:%[i1]\n\t"
+      "ds_read_b128 %[f8], %[t0] offset:%[i2]\n\t"
+      "ds_read_b128 %[f12], %[t0] offset:%[i3]\n\t"
+      "v_xor_b32 %[t1], 64, %[ka]\n\t"
+      "ds_read_b128 %[f1], %[t1] offset:%[i0]\n\t"
+      "ds_read_b128 %[f5], %[t1] offset:%[i1]\n\t"
+      "ds_read_b128 %[f9], %[t1] offset:%[i2]\n\t"
+      "ds_read_b128 %[f13], %[t1] offset:%[i3]\n\t"
+      "v_xor_b32 %[t0], 128, %[ka]\n\t"
+      "ds_read_b128 %[f2], %[t0] offset:%[i0]\n\t"
+      "ds_read_b128 %[f6], %[t0] offset:%[i1]\n\t"
+      "ds_read_b128 %[f10], %[t0] offset:%[i2]\n\t"
+      "ds_read_b128 %[f14], %[t0] offset:%[i3]\n\t"
+      "v_xor_b32 %[t1], 192, %[ka]\n\t"
+      "ds_read_b128 %[f3], %[t1] offset:%[i0]\n\t"
+      "ds_read_b128 %[f7], %[t1] offset:%[i1]\n\t"
+      "ds_read_b128 %[f11], %[t1] offset:%[i2]\n\t"
+      "ds_read_b128 %[f15], %[t1] offset:%[i3]"
+      : [t0] "=&v"(t0), [t1] "=&v"(t1),
+        [f0] "=&a"(kf[0]), [f1] "=&a"(kf[1]), [f2] "=&a"(kf[2]), [f3] "=&a"(kf[3]), [f4]
+        "=&a"(kf[4]), [f5] "=&a"(kf[5]), [f6] "=&a"(kf[6]), [f7] "=&a"(kf[7]), [f8]
+        "=&a"(kf[8]), [f9] "=&a"(kf[9]), [f10] "=&a"(kf[10]), [f11] "=&a"(kf[11]), [f12]
+        "=&a"(kf[12]), [f13] "=&a"(kf[13]), [f14] "=&a"(kf[14]), [f15] "=&a"(kf[15])
+      : [ka] "v"(k_addr), [i0] "i"(kImm), [i1] "i"(kImm + 256), [i2] "i"(kImm + 512),
+        [i3] "i"(kImm + 768));
+}
+// Issue position of k-step s in d512_read_kfrags.
+constexpr int d512FragPos(int s) { return 4 * (s & 3) + (s >> 2); }
+template <int kStep>
+__device__ __forceinline__ void d512_kfrag_ready(u32x4v_t &f) {
+  asm volatile("s_waitcnt lgkmcnt(%[n])" : "+a"(f) : [n] "i"(15 - d512FragPos(kStep)));
+}
+template <int kBegin, int kEnd, class F>
+__device__ __forceinline__ void d512_static_for(F &&f) {
+  if constexpr (kBegin < kEnd) {
+    f(std::integral_constant<int, kBegin>{});
+    d512_static_for<kBegin + 1, kEnd>(f);
+  }
 }
 
 __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Params p) {
@@ -169,6 +231,14 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       qreg[s] = row_ok ? load128(qrow + 32 * s + 8 * g) : make_uint4(0, 0, 0, 0);
+    // Q lives in AGPRs (an MFMA operand may be an AGPR); all loads are
+    // issued before the first constraint forces a wait.
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4v_t t4 = {qreg[s].x, qreg[s].y, qreg[s].z, qreg[s].w};
+      asm volatile("" : "+a"(t4));
+      qreg[s] = make_uint4(t4.x, t4.y, t4.z, t4.w);
+    }
   }
 
   float m_run = -INFINITY, l_run = 0.0f;
@@ -195,6 +265,10 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
                     wave_uniform(dv));
     }
   };
+  const int k15 = lane & 15;
+  const uint32_t k_base = lds_address(&lds.k[0][0]) + k15 * kD512RowBytes +
+                          16 * (g ^ (k15 & 3)) + 64 * ((k15 >> 2) & 3);
+  constexpr int kStageBytes = kD512Tile * kD512RowBytes;
   copy_tile(0, 0);
   for (int tile = 0; tile < n_tiles; ++tile) {
     const int kt = tile * kD512Tile;
@@ -205,23 +279,33 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
     __syncthreads();
     if (tile + 1 < n_tiles) copy_tile(kt + kD512Tile, stage ^ 1);
     if (!row_ok || kt > row) continue;  // uniform per wave
-    const uint4 *s_k = lds.k[stage];
     const uint4 *s_v = lds.v[stage];
 
     // Scores of the two 16-key blocks: lane holds head `head`, keys
     // 16 blk + 4 g + i.
     f32x4_t sblk[2];
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const int key = 16 * blk + (lane & 15);
-      f32x4_t s_acc = f32x4_t{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int c = 4 * s + g;
-        const uint4 kf = s_k[key * kD512Chunks + (c ^ (key & 15))];
-        s_acc = mfma16(kf, qreg[s], s_acc);
-      }
-      sblk[blk] = s_acc;
+    auto score_block = [&](auto st, auto bl) __attribute__((always_inline)) {
+      constexpr int kImm =
+          decltype(st)::value * kStageBytes + decltype(bl)::value * 16 * kD512RowBytes;
+      u32x4v_t kf[16];
+      d512_read_kfrags<kImm>(k_base, kf);
+      f32x4_t s2[2] = {f32x4_t{}, f32x4_t{}};
+      d512_static_for<0, 16>([&](auto pc) __attribute__((always_inline)) {
+        constexpr int pos = decltype(pc)::value;
+        constexpr int s = 4 * (pos & 3) + (pos >> 2);  // k-step at issue position pos
+        d512_kfrag_ready<s>(kf[s]);
+        s2[pos & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8_t, kf[s]), __builtin_bit_cast(bf16x8_t, qreg[s]),
+            s2[pos & 1], 0, 0, 0);
+      });
+      return s2[0] + s2[1];
+    };
+    if (stage == 0) {
+      sblk[0] = score_block(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{});
+      sblk[1] = score_block(std::integral_constant<int, 0>{}, std::integral_constant<int, 1>{});
+    } else {
+      sblk[0] = score_block(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{});
+      sblk[1] = score_block(std::integral_constant<int, 1>{}, std::integral_constant<int, 1>{});
     }
     float sc[8];
     float tmax = -INFINITY;
@@ -274,6 +358,16 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
       acc[d] = mfma16(make_uint4(half_op[0].x, half_op[0].y, half_op[1].x, half_op[1].y), pb,
                       acc[d]);
     }
+    // Keep the transposing V reads kD512VLead MFMAs ahead of their MFMA
+    // (measured: 2 ahead 171 us, 4 ahead 164 us, 6 ahead 164.7 us for the
+    // 2048-row launcher).
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kD512VLead, 1);
+#pragma unroll
+    for (int i = 0; i < DB - kD512VLead; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // its successor's 2 reads
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, kD512VLead, 1);
   }
 
   wait_copies();  // no copy may still be writing LDS when the workgroup exits

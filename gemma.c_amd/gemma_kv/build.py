@@ -31,12 +31,13 @@ HIP_FLAGS = [
 ]
 
 
-# Per-source additions. The prefill kernel rescales its MFMA accumulators with
+# Per-source additions. The prefill kernels rescale their MFMA accumulators with
 # VALU multiplies on a rarely taken path; in the AGPR form the register
 # allocator copies all 128 accumulators between AGPRs and VGPRs on every tile
-# to serve that path, so its MFMAs are selected in the VGPR form.
+# to serve that path, so their MFMAs are selected in the VGPR form.
 EXTRA_FLAGS = {
     "prefill_attention": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
+    "prefill_norm_rope": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"],
 }
 
 
