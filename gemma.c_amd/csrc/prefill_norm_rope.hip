@@ -65,7 +65,11 @@ struct PrefillPrepParams {
 // head; a wave first loads its head of all kPrepRows rows, then prepares
 // and stores them one by one, so the row loads overlap. A negative
 // position skips the row (src/gemma4_flash_attention_prefill.cu:1049-1051).
-constexpr int kPrepRows = 8;
+// Two rows per workgroup: more, smaller workgroups measured faster for
+// 2048 rows (launchers 8x256 / 1x512: 8 rows 67.5 / 164 us, 4 rows 64.5 /
+// 157.3 us, 2 rows 63.5 / 157.4 us, 1 row 63.2 / 157.2 us, 16 rows 69.7 /
+// 183.6 us).
+constexpr int kPrepRows = 2;
 
 template <int kHeads, int kDim, int kRotary, bool kHasV>
 __global__ __launch_bounds__((prep_waves<kHeads, kHasV>() * kWave)) void prefill_prep_kernel(
