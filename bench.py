@@ -320,6 +320,17 @@ def bench_prefill(torch, gk, dev, reps):
         # time-based warm-up (50 short chunks are shorter than the clock ramp).
         warm_clock(torch, fn)
         ms = time_eager(torch, fn, max(reps, 50), 10)
+        plain_ms = None
+        if not window and raw is not gk.lib().gemma4_flash_attention_prefill_chunk_paged_bf16:
+            # The same chunk through the entry point without a workspace.
+            plain = gk.lib().gemma4_flash_attention_prefill_chunk_paged_bf16
+            plain_args = args[:13]
+
+            def fn_plain(st):
+                code = plain(*plain_args, st)
+                if code:
+                    raise gk.HipError(code, "prefill")
+            plain_ms = time_eager(torch, fn_plain, max(reps, 50), 10)
         keys = np.arange(lq) + prior + 1
         if window:
             keys = np.minimum(keys, window)
@@ -328,6 +339,9 @@ def bench_prefill(torch, gk, dev, reps):
         res[kind] = {"us_per_chunk": round(ms * 1e3, 2), "gflop": round(flops / 1e9, 2),
                      "tflops": round(tflops, 1),
                      "mfma_util_vs_bf16_dense_peak": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)}
+        if plain_ms is not None:
+            res[kind]["entry_point"] = "gemma4_flash_attention_prefill_chunk_paged_bf16_ws (balanced)"
+            res[kind]["us_per_chunk_unbalanced"] = round(plain_ms * 1e3, 2)
     return res
 
 
