@@ -90,14 +90,18 @@ struct PrefillParams {
   float q_scale;             // softmax_scale * log2(e)
   // Balanced global chunks (n_pairs > 0): row blocks j and nb-1-j form a
   // pair served by two workgroups with equal key work; the one row block a
-  // pair splits meets in ws_partial (per split slot, two halves of
-  // kPartialFloats x 256 floats) and ws_counters (arrivals, re-armed to 0).
+  // pair splits meets in its slot of the workspace.
   int32_t n_pairs;
-  float *ws_partial;
-  int32_t *ws_counters;
+  char *ws;
 };
 
 constexpr int kPartialFloats = 130;  // per thread: 128 accumulators, max, sum
+// Workspace slot s at s * kSlotBytes: the arrival counter (256-byte
+// aligned), then the two halves' partials (kPartialFloats x 256 floats
+// each, element-major). A slot sits at the same place for every chunk
+// length, so calls of different sizes can share a workspace.
+constexpr int64_t kSlotCounterBytes = 256;
+constexpr int64_t kSlotBytes = kSlotCounterBytes + 2LL * kPartialFloats * kPrefillThreads * 4;
 
 __device__ __forceinline__ f32x16_t mfma32(uint4 a, uint4 b, f32x16_t c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -614,9 +618,10 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   // second arriver merge both halves and write the rows.
   bool emit = true;
   if (unit_slot >= 0) {
-    float *mine = p.ws_partial + ((int64_t)unit_slot * 2 + unit_part) * kPartialFloats * kPrefillThreads;
-    const float *other =
-        p.ws_partial + ((int64_t)unit_slot * 2 + (unit_part ^ 1)) * kPartialFloats * kPrefillThreads;
+    char *slot = p.ws + (int64_t)unit_slot * kSlotBytes;
+    float *part = reinterpret_cast<float *>(slot + kSlotCounterBytes);
+    float *mine = part + unit_part * kPartialFloats * kPrefillThreads;
+    const float *other = part + (unit_part ^ 1) * kPartialFloats * kPrefillThreads;
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -631,7 +636,7 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
     __syncthreads();
     if (t == 0) {
-      int32_t *counter = p.ws_counters + unit_slot;
+      int32_t *counter = reinterpret_cast<int32_t *>(slot);
       const int32_t arrived =
           __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (arrived == 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -691,18 +696,15 @@ using namespace gemma4;
 namespace {
 
 // Balanced-mode geometry of a chunk: row-block pairs per (sequence, head) and
-// the workspace bytes: arrival counters (256-byte aligned), then two partial
-// halves per split slot.
+// the workspace bytes (one slot per pair).
 int prefill_pairs(int32_t chunk_len) {
   const int nb = (chunk_len + kPrefillRows - 1) / kPrefillRows;
   return nb < 2 ? 0 : (nb + 1) / 2;
 }
-size_t prefill_counter_bytes(int64_t slots) { return (size_t)((slots * 4 + 255) / 256 * 256); }
 size_t prefill_workspace_bytes(int32_t batch_size, int32_t chunk_len, int32_t heads) {
   if (batch_size <= 0 || chunk_len <= 0 || heads <= 0) return 0;
   const int64_t slots = (int64_t)batch_size * heads * prefill_pairs(chunk_len);
-  if (slots == 0) return 0;
-  return prefill_counter_bytes(slots) + (size_t)slots * 2 * kPartialFloats * kPrefillThreads * 4;
+  return (size_t)(slots * kSlotBytes);
 }
 
 hipError_t prefill_chunk_launch(gemma4_bf16 *d_out, const gemma4_bf16 *d_q, const gemma4_bf16 *d_k,
@@ -752,16 +754,9 @@ hipError_t prefill_chunk_launch(gemma4_bf16 *d_out, const gemma4_bf16 *d_q, cons
   // Sliding chunks already carry equal work per row block; only causal
   // (global) chunks of two or more row blocks are paired.
   p.n_pairs = balanced && config.window_size == 0 ? prefill_pairs(chunk_len) : 0;
-  p.ws_counters = nullptr;
-  p.ws_partial = nullptr;
+  p.ws = p.n_pairs > 0 ? static_cast<char *>(d_workspace) : nullptr;
   int blocks = config.num_heads * ((chunk_len + kPrefillRows - 1) / kPrefillRows);
-  if (p.n_pairs > 0) {
-    const int64_t slots = (int64_t)batch_size * config.num_heads * p.n_pairs;
-    p.ws_counters = static_cast<int32_t *>(d_workspace);
-    p.ws_partial = reinterpret_cast<float *>(static_cast<char *>(d_workspace) +
-                                             prefill_counter_bytes(slots));
-    blocks = config.num_heads * 2 * p.n_pairs;
-  }
+  if (p.n_pairs > 0) blocks = config.num_heads * 2 * p.n_pairs;
   if (p.n_pairs > 0) {
     hipLaunchKernelGGL(prefill_chunk_kernel<true>, dim3(blocks, batch_size),
                        dim3(kPrefillThreads), 0, stream, p);

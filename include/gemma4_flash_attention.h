@@ -161,8 +161,9 @@ hipError_t gemma4_flash_attention_prefill_chunk_paged_bf16(
 // up to float summation order. d_workspace: at least
 // gemma4_flash_attention_prefill_chunk_workspace_bytes(batch_size,
 // chunk_len, config) bytes, 256-byte aligned, zero-filled once before its
-// first use (every call leaves its arrival counters at zero again); calls
-// that share a workspace must not overlap. Sliding chunks (window > 0) run
+// first use (every call leaves its arrival counters at zero again); one
+// sized for the largest chunk and batch also serves every smaller call;
+// calls that share a workspace must not overlap. Sliding chunks (window > 0) run
 // the plain kernel and ignore the workspace. No counterpart in the
 // reference, whose prefill launcher (src/gemma4_flash_attention_prefill.cu:
 // 1131-1183) assigns one causal row block per block.

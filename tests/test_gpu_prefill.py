@@ -13,6 +13,7 @@ from oracle import oracle
 
 pytestmark = pytest.mark.gpu
 H, D = 8, 256
+SLOT_BYTES = 256 + 2 * 130 * 256 * 4  # balanced-prefill workspace slot
 
 
 def _full_keys(cache, cfg, pt, b, prior, chunk):
@@ -128,9 +129,25 @@ def test_prefill_balanced_global_matches_oracle(dev, priors, lq, page):
     assert_close(got, plain, f"balanced vs plain priors={priors} lq={lq}")
     got2, _, exp2, _ = _run_balanced(dev, rng, priors[:1], max(lq // 2, 65), page, ws)
     assert_close(got2, exp2, f"balanced second call priors={priors[:1]}")
-    pairs = ((lq + 63) // 64 + 1) // 2
-    counter_bytes = (len(priors) * H * pairs * 4 + 255) // 256 * 256
-    assert not ws[:counter_bytes].any().item()  # every arrival counter re-armed to zero
+    # Every slot's arrival counter (the first word of the slot) is re-armed to zero.
+    slots = ws[: ws.numel() // SLOT_BYTES * SLOT_BYTES].view(-1, SLOT_BYTES)
+    assert not slots[:, :4].any().item()
+
+
+def test_prefill_balanced_workspace_shared_by_chunk_sizes(dev):
+    """A workspace sized for the largest chunk serves a large, a small and
+    again a large chunk: each slot keeps its place whatever the chunk
+    length, so a small call's partials never land on a counter a larger
+    call reads."""
+    import torch
+    rng = np.random.default_rng(77)
+    cfg = gk.make_config(*cache_config(1, 1, 16, 33, H, D, 0))
+    ws = torch.zeros(gk.flash_attention_prefill_chunk_workspace_bytes(1, 512, cfg),
+                     dtype=torch.uint8, device=dev)
+    for lq, prior in ((512, 0), (130, 40), (512, 9)):
+        got, plain, exp, _ = _run_balanced(dev, rng, [prior], lq, 16, ws)
+        assert_close(got, exp, f"shared workspace lq={lq}")
+        assert_close(got, plain, f"shared workspace vs plain lq={lq}")
 
 
 def test_prefill_balanced_argument_checks(dev):
@@ -139,8 +156,8 @@ def test_prefill_balanced_argument_checks(dev):
     sliding = gk.make_config(*cache_config(1, 1, 16, 4, H, D, 32))
     lq = 256
     nbytes = gk.flash_attention_prefill_chunk_workspace_bytes(1, lq, cfg)
-    # Counters (256-byte block) + 2 pairs x 8 heads x 2 halves x 130 x 256 floats.
-    assert nbytes == 256 + 2 * 8 * 2 * 130 * 256 * 4
+    # 2 pairs x 8 heads = 16 slots: a 256-byte counter + 2 halves x 130 x 256 floats each.
+    assert nbytes == 16 * SLOT_BYTES
     assert gk.flash_attention_prefill_chunk_workspace_bytes(1, lq, sliding) == 0
     assert gk.flash_attention_prefill_chunk_workspace_bytes(1, 64, cfg) == 0  # one row block
     x = torch.zeros((1, lq, 16, D), dtype=torch.int16, device=dev)
