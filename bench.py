@@ -1043,7 +1043,6 @@ def main():
                      "timing": "median of single launches between HIP events on the launch stream",
                      "algorithmic_bytes_per_launch": step_bytes},
     }
-    result["config1_gpu"] = bench_config1(torch, gk, dev)
     result["step_reference_global_geometry"] = bench_step_ref_geometry(
         torch, gk, dev, layers, caches, meta, max(10, args.steps // 2))
     if not args.no_batch64:
@@ -1056,12 +1055,14 @@ def main():
     del runner, kv_b64, kv_long
     if not args.no_prefill:
         result["prefill_config5"] = bench_prefill(torch, gk, dev, max(5, args.steps // 2))
+    # The legs timed by graph replay come last. Each graph leg also runs on a
+    # second stream (warm-up outside capture, the capture itself); once a
+    # kernel has run on another stream, the eager launches of the first
+    # measured 4-5% slower for the rest of the process (long context 157.6
+    # -> 164.8 us after one small kernel on a side stream).
+    result["config1_gpu"] = bench_config1(torch, gk, dev)
     if not args.no_widened:
         result["widened"] = bench_widened(torch, gk, dev)
-    # The legs timed by graph replay come last: once the 8x256 split kernel
-    # has been replayed from a graph, its later eager launches in the same
-    # process measured 4-5% slower (long context 157.8 -> 164.9 us) and
-    # stayed so after the graph was freed.
     rounds = 20
     g_ms, _ = time_graph(torch, lambda st: [split_round(g_layers)(st) for _ in range(rounds)], 3, 1)
     s_ms, _ = time_graph(torch, lambda st: [split_round(s_layers)(st) for _ in range(4)], 3, 1)
