@@ -736,15 +736,20 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
 
 // Log-sum-exp combine of the live splits of one (batch, query head) row
 // (src/gemma4_flash_attention_decode.cu:880-977), as a separate launch.
-// Workgroup (row, 64-dim block): 256 threads = 16 split lanes x 16 groups of
-// 4 dims. Each thread folds its splits (s = lane, lane + 16, ...) into a
-// running (max, sum, acc) as it streams them -- the loads do not depend on
-// the arithmetic, so they are all in flight together -- and the 16 split
-// lanes are merged the same way through LDS. Empty splits (l = 0) weigh 0;
-// a row without a live split is zeros.
+// Workgroup (row, block of combine_dims dims): 256 threads = split lanes x
+// groups of 4 dims (16 x 16 for 256-dim rows, 32 x 8 for 512-dim rows).
+// Each thread folds its splits (s = lane, lane + lanes, ...) into a running
+// (max, sum, acc) as it streams them -- the loads do not depend on the
+// arithmetic, so they are all in flight together -- and the split lanes are
+// merged the same way through LDS. Empty splits (l = 0) weigh 0; a row
+// without a live split is zeros.
 constexpr int kCombineThreads = 256;
-constexpr int kCombineDims = 64;
-constexpr int kCombineLanes = kCombineThreads / (kCombineDims / 4);  // split lanes
+// Dims per workgroup: 64 for 256-dim rows (16 split lanes), 32 for 512-dim
+// rows (32 split lanes: the 1 x 512 layer's ~129 splits fold in shorter
+// chains; 24.0 against 24.8 us per layer, while 32 dims for 256-dim rows
+// measured ~1% slower on the per-layer and batch-64 legs).
+template <int kDim>
+constexpr int combine_dims() { return kDim == 512 ? 32 : 64; }
 
 template <int kDim>
 __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
@@ -752,6 +757,8 @@ __global__ __launch_bounds__(kCombineThreads) void decode_combine_kernel(
     const float *__restrict__ partial_l, const float *__restrict__ partial_acc,
     const int32_t *__restrict__ seq_lengths, int32_t window_size,
     int32_t split_size, int32_t num_splits, const int32_t *__restrict__ gate) {
+  constexpr int kCombineDims = combine_dims<kDim>();
+  constexpr int kCombineLanes = kCombineThreads / (kCombineDims / 4);  // split lanes
   __shared__ float s_m[kCombineLanes], s_l[kCombineLanes];
   __shared__ float4 s_a[kCombineLanes][kCombineDims / 4];
   const int t = threadIdx.x;
@@ -858,7 +865,7 @@ hipError_t launch_decode(const DecodeParams &p, int32_t batch_count, bool combin
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !combine || p.num_splits == 1 || p.counters != nullptr) return e;
   hipLaunchKernelGGL(decode_combine_kernel<D>,
-                     dim3(batch_count * kQueryHeads, D / kCombineDims),
+                     dim3(batch_count * kQueryHeads, D / combine_dims<D>()),
                      dim3(kCombineThreads), 0, stream, p.out, p.partial_m, p.partial_l,
                      p.partial_acc, p.seq_lengths, p.c.window_size, p.split_size,
                      p.num_splits, p.gate);
@@ -1096,12 +1103,12 @@ hipError_t gemma4_flash_attention_decode_combine_bf16(
   uint16_t *out = reinterpret_cast<uint16_t *>(d_out);
   const dim3 block(kCombineThreads);
   if (config.head_dim == 256) {
-    hipLaunchKernelGGL(decode_combine_kernel<256>, dim3(batch_count * kQueryHeads, 256 / kCombineDims),
+    hipLaunchKernelGGL(decode_combine_kernel<256>, dim3(batch_count * kQueryHeads, 256 / combine_dims<256>()),
                        block, 0, stream, out, d_partial_m, d_partial_l, d_partial_acc,
                        d_seq_lengths, config.window_size, split_size, num_splits,
                        static_cast<const int32_t *>(nullptr));
   } else if (config.head_dim == 512) {
-    hipLaunchKernelGGL(decode_combine_kernel<512>, dim3(batch_count * kQueryHeads, 512 / kCombineDims),
+    hipLaunchKernelGGL(decode_combine_kernel<512>, dim3(batch_count * kQueryHeads, 512 / combine_dims<512>()),
                        block, 0, stream, out, d_partial_m, d_partial_l, d_partial_acc,
                        d_seq_lengths, config.window_size, split_size, num_splits,
                        static_cast<const int32_t *>(nullptr));
