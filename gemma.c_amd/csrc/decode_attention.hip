@@ -845,6 +845,18 @@ bool valid_decode_config(const Gemma4KvCacheConfig &c, int32_t layer) {
          (c.window_size == 0 || capacity >= c.window_size) && rows < (1ll << 31);
 }
 
+}  // namespace
+
+bool decode_geometry_ok(const Gemma4KvCacheConfig &c, int32_t layer, int32_t batch_count,
+                        int32_t split_size, int32_t num_splits) {
+  return batch_count > 0 && batch_count <= c.batch_size && batch_count <= 65535 &&
+         num_splits > 0 && num_splits <= 65535 && split_size > 0 &&
+         valid_decode_config(c, layer) &&
+         ((c.num_heads == 8 && c.head_dim == 256) || (c.num_heads == 1 && c.head_dim == 512));
+}
+
+namespace {
+
 template <class Sh>
 int waves_for(int32_t split_size) {
   const int chunks = (split_size + Sh::CT * Sh::KT - 1) / (Sh::CT * Sh::KT);
@@ -884,9 +896,8 @@ hipError_t decode_entry(uint16_t *out, float *pm, float *pl, float *pacc,
                         const uint16_t *k_norm_weight = nullptr, const float *cos = nullptr,
                         const float *sin = nullptr, const int32_t *gate = nullptr) {
   if (batch_count == 0) return hipSuccess;
-  if (batch_count < 0 || batch_count > c.batch_size || batch_count > 65535 || num_splits > 65535 ||
-      !valid_decode_config(c, layer) || !(softmax_scale > 0.0f) ||
-      split_size <= 0 || num_splits <= 0 || out == nullptr || q == nullptr ||
+  if (!decode_geometry_ok(c, layer, batch_count, split_size, num_splits) ||
+      !(softmax_scale > 0.0f) || out == nullptr || q == nullptr ||
       cache_k == nullptr || cache_v == nullptr || page_table == nullptr ||
       seq_lengths == nullptr) {
     return hipErrorInvalidValue;
@@ -1018,8 +1029,10 @@ hipError_t gemma4_flash_attention_append_decode_paged_bf16_noalloc(
     Gemma4KvCacheConfig config, int32_t layer, float softmax_scale, int32_t split_size,
     int32_t num_splits, int32_t batch_count, hipStream_t stream) {
   if (batch_count == 0) return hipSuccess;
+  // Range checks come before the scratch-size product so it cannot overflow.
   if (d_token_position == nullptr || d_k == nullptr || d_v == nullptr || batch_count < 0 ||
-      num_splits <= 0 || (config.head_dim != 256 && config.head_dim != 512)) {
+      batch_count > 65535 || num_splits <= 0 || num_splits > 65535 ||
+      (config.head_dim != 256 && config.head_dim != 512)) {
     return hipErrorInvalidValue;
   }
   // Partials of this call: m and l [rows * splits], acc [rows * splits * D].

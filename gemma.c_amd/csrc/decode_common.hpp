@@ -184,6 +184,11 @@ __device__ __forceinline__ auto coherent_view(const float *p, int32_t count) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(p), 0, count * 4, 0x00020000);
 }
 
+// Whether a decode entry point accepts this cache geometry, cache layer,
+// batch and split plan (the checks decode_entry makes before any launch).
+bool decode_geometry_ok(const Gemma4KvCacheConfig &c, int32_t layer, int32_t batch_count,
+                        int32_t split_size, int32_t num_splits);
+
 // The fused append + split-K decode with the separate combine
 // (decode_attention.hip) for the persistent step's 1 x 512 global layers:
 // while the word at `gate` (the step workspace's status) is nonzero the

@@ -1043,8 +1043,9 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
 // 157 KB of LDS a workgroup takes leaves room for no second one on a CU).
 // The steps are ordinary launches by default: a cooperative launch costs
 // ~18 us more per step to dispatch (405 vs 387 us per config-2 step), and
-// HIP serves it from a dedicated queue whose teardown at process exit
-// crashed every profiled run that had made one. Callers that share the GPU
+// every run under rocprofv3 that had made a cooperative launch crashed in
+// exit() (cause not established; runs with ordinary launches only exit
+// cleanly). Callers that share the GPU
 // with other work can ask for cooperative step launches
 // (gemma4_decode_step_set_cooperative), which the runtime admits only with
 // all workgroups resident. Otherwise, should another kernel hold CUs during
@@ -1167,14 +1168,11 @@ extern "C" hipError_t gemma4_decode_step_inject_stall(void *workspace, int32_t l
 namespace gemma4 {
 namespace {
 
-// One persistent launch over model layers [first_layer, first_layer + count),
-// all of them in 8 x 256 caches.
-hipError_t step_run(uint16_t *out, const uint16_t *q, const uint16_t *k, const uint16_t *v,
-                    gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
-                    const int32_t *const pt[2], const Gemma4KvCacheConfig cfg[2],
-                    const int32_t *seq_lengths, const int32_t *token_position,
-                    int32_t first_layer, int32_t layer_count, float scale,
-                    int32_t batch_count, void *workspace, hipStream_t stream) {
+// Whether the persistent kernel accepts model layers [first_layer,
+// first_layer + layer_count), all of them in 8 x 256 caches (no launch).
+hipError_t step_check(gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
+                      const int32_t *const pt[2], const Gemma4KvCacheConfig cfg[2],
+                      int32_t first_layer, int32_t layer_count, int32_t batch_count) {
   const WorkspaceLayout w = workspace_layout(batch_count);
   bool need_kind[2] = {false, false};
   for (int32_t l = first_layer; l < first_layer + layer_count; ++l)
@@ -1191,6 +1189,20 @@ hipError_t step_run(uint16_t *out, const uint16_t *q, const uint16_t *k, const u
     const int64_t rows = (int64_t)c.num_layers * c.num_pages * c.page_size;
     if (rows * kRowElems >= (int64_t)1 << 31 || c.num_layers < 1) return hipErrorInvalidValue;
   }
+  return hipSuccess;
+}
+
+// One persistent launch over model layers [first_layer, first_layer + count),
+// all of them in 8 x 256 caches.
+hipError_t step_run(uint16_t *out, const uint16_t *q, const uint16_t *k, const uint16_t *v,
+                    gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
+                    const int32_t *const pt[2], const Gemma4KvCacheConfig cfg[2],
+                    const int32_t *seq_lengths, const int32_t *token_position,
+                    int32_t first_layer, int32_t layer_count, float scale,
+                    int32_t batch_count, void *workspace, hipStream_t stream) {
+  const hipError_t ok = step_check(ck, cv, pt, cfg, first_layer, layer_count, batch_count);
+  if (ok != hipSuccess) return ok;
+  const WorkspaceLayout w = workspace_layout(batch_count);
   StepParams p = base_params(workspace, w, batch_count);
   p.out = out;
   p.q = q;
@@ -1266,6 +1278,25 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
                                                   kRefTargetWorkgroups, &ref_split, &ref_splits);
     if (e != hipSuccess) return e;
     if ((int64_t)batch_count * ref_splits > kRefPartialSlots) return hipErrorInvalidValue;
+  }
+  // Everything is checked before the first launch, so a rejected call
+  // leaves every cache and output untouched: each run of sliding layers as
+  // the persistent kernel will see it, each global layer as its launch will.
+  for (int32_t l = first_layer; l < last;) {
+    if (is_global(l)) {
+      if (global_cache_k == nullptr || global_cache_v == nullptr ||
+          global_page_table == nullptr ||
+          !decode_geometry_ok(global_config, gemma4_kv_cache_layer_index(l, true), batch_count,
+                              ref_split, ref_splits))
+        return hipErrorInvalidValue;
+      ++l;
+      continue;
+    }
+    int32_t run = 0;
+    while (l + run < last && !is_global(l + run)) ++run;
+    const hipError_t e = step_check(ck, cv, pt, cfg, l, run, batch_count);
+    if (e != hipSuccess) return e;
+    l += run;
   }
   const WorkspaceLayout w = workspace_layout(batch_count);
   int32_t *ints = static_cast<int32_t *>(workspace);

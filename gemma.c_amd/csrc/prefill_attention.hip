@@ -636,15 +636,19 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
     __builtin_amdgcn_s_waitcnt(0);  // this thread's stores have completed
     __syncthreads();
     if (t == 0) {
+      // Release: the workgroup's partial stores (complete at the barrier)
+      // are ordered before the arrival; acquire: the first arriver's partial
+      // is visible to the second arriver.
       int32_t *counter = reinterpret_cast<int32_t *>(slot);
       const int32_t arrived =
-          __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_fetch_add(counter, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
       if (arrived == 1) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = arrived == 1 ? 1 : 0;
     }
     __syncthreads();
     emit = s_last != 0;
     if (emit) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       const float mo = __hip_atomic_load(other + 128 * kPrefillThreads + t, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT);
       const float lo = __hip_atomic_load(other + 129 * kPrefillThreads + t, __ATOMIC_RELAXED,

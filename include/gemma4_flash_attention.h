@@ -284,8 +284,10 @@ hipError_t gemma4_decode_step_status_async(const void *workspace, int32_t *statu
 // reference): 0 (default) ordinary launches; 1 cooperative launches, which
 // the runtime admits only with all 256 workgroups resident -- for callers
 // that share the GPU with other kernels -- at ~18 us more dispatch cost per
-// step. (A process that has made a cooperative launch has been seen to
-// crash at exit under rocprofv3.)
+// step. Do not run a process that makes cooperative step launches under
+// rocprofv3: every profiled run that made a cooperative launch crashed with
+// SIGSEGV in exit() after the profiler had written its files; the cause of
+// that crash has not been established, and ordinary launches avoid it.
 hipError_t gemma4_decode_step_set_cooperative(int32_t enable);
 // Fault injection for tests (no counterpart in the reference): from the next
 // launch on, at launch-relative layer `layer` one workgroup waits for a

@@ -419,3 +419,38 @@ def test_decode_step_config2_matches_per_layer_path(dev):
     torch.cuda.synchronize()
     assert gk.decode_step_status(ws) == 0
     assert torch.equal(out2, out)
+
+
+def test_decode_step_reference_geometry_rejects_before_any_launch(dev):
+    """With 1 x 512 global layers the step is several launches; a bad argument
+    of any of them is rejected before the first one, so nothing is appended
+    and no output row is written. Case 1: first layer 5 (global) with a bad
+    sliding config for layer 6. Case 2: a global config whose num_layers
+    covers global layer 5 but not 11."""
+    import torch
+    c = _ref_case(np.random.default_rng(77), 5, 7, [151], 64, 1, 16)
+    d = {n: to_dev(a, dev) for n, a in c["caches"].items()}
+    ws = _workspace(dev, 1)
+    total = sum(16 * w for _, w in c["geo"])
+    out = torch.full((total,), 0x1234, dtype=torch.int16, device=dev)
+    seq = to_dev(np.asarray(c["seq"], np.int32), dev)
+    pos = to_dev(np.asarray(c["pos"], np.int32), dev)
+
+    def call(s_cfg, g_cfg):
+        return gk.decode_step_layers_bf16(
+            out, to_dev(c["q"], dev), to_dev(c["k"], dev), to_dev(c["v"], dev), d["sk"],
+            d["sv"], to_dev(c["s_pt"], dev), gk.make_config(*s_cfg), d["gk"], d["gv"],
+            to_dev(c["g_pt"], dev), gk.make_config(*g_cfg), seq, pos, 5, 7, c["scale"], 1, ws)
+
+    bad_sliding = list(c["s_cfg"])
+    bad_sliding[6] = 128  # head_dim the persistent kernel does not serve
+    short_global = list(c["g_cfg"])
+    short_global[0] = 1   # global cache layer 1 (model layer 11) out of range
+    for s_cfg, g_cfg in ((bad_sliding, c["g_cfg"]), (c["s_cfg"], short_global)):
+        assert call(s_cfg, g_cfg) == gk.HIP_ERROR_INVALID_VALUE
+        torch.cuda.synchronize()
+        assert (out == 0x1234).all()
+        for n in c["caches"]:
+            assert np.array_equal(from_dev_bf16(d[n]).reshape(c["caches"][n].shape),
+                                  c["caches"][n]), n
+    assert gk.decode_step_status(ws) == 0

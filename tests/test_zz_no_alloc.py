@@ -105,6 +105,35 @@ def test_noalloc_single_split_writes_directly(dev):
     assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
 
 
+def test_noalloc_allocates_no_device_memory(dev):
+    """After a warm-up call (which looks up the scratch address once), a
+    further call leaves the device's free memory unchanged."""
+    import torch
+    rng = np.random.default_rng(11)
+    seq = [2000, 513]
+    cfg, pt, ck, cv, q, k, v = _case(rng, seq, 8, 256, 0, 16)
+    conf = gk.make_config(*cfg)
+    split, n = gk.decode_split_plan(conf, len(seq), max(seq))
+    assert n > 1
+    d_seq = to_dev(np.asarray(seq, np.int32), dev)
+    d_pos = to_dev(np.asarray([s - 1 for s in seq], np.int32), dev)
+    d_pt, d_q, d_k, d_v = to_dev(pt, dev), to_dev(q, dev), to_dev(k, dev), to_dev(v, dev)
+    c_k, c_v = to_dev(ck, dev), to_dev(cv, dev)
+    out = torch.zeros((len(seq), 16, 256), dtype=torch.int16, device=dev)
+
+    def call():
+        gk.check(gk.flash_attention_append_decode_paged_bf16_noalloc(
+            out, d_q, c_k, c_v, d_pt, d_seq, d_pos, d_k, d_v, conf, 0, 0.0625, split, n,
+            len(seq)), "noalloc")
+        torch.cuda.synchronize()
+
+    call()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        call()
+    assert torch.cuda.mem_get_info()[0] == free0
+
+
 def test_noalloc_rejects_calls_past_the_scratch(dev):
     import torch
     conf = gk.make_config(1, 64, 64, 1, 64, 8, 256, 0)
@@ -114,4 +143,11 @@ def test_noalloc_rejects_calls_past_the_scratch(dev):
     code = gk.flash_attention_append_decode_paged_bf16_noalloc(
         dummy, dummy, dummy, dummy, i32, i32, i32, dummy, dummy, conf, 0, 0.0625, 64, 1024, 64)
     assert code == HIP_ERROR_OUT_OF_MEMORY
+    # Counts past the entry point's limits are refused before the scratch
+    # size is computed.
+    for batch, splits in ((70000, 2), (1, 70000)):
+        code = gk.flash_attention_append_decode_paged_bf16_noalloc(
+            dummy, dummy, dummy, dummy, i32, i32, i32, dummy, dummy, conf, 0, 0.0625, 64,
+            splits, batch)
+        assert code == gk.HIP_ERROR_INVALID_VALUE
     torch.cuda.synchronize()
