@@ -196,6 +196,20 @@ __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memr
   } while (0)
 #endif
 
+// Development builds only (-DSTEP_FLOOR=n): the same launch with parts of
+// the work taken out, to price the per-layer handoffs on their own.
+//   1: no K/V bytes -- no cache tiles, no LDS DMA, no appended row; every
+//      exchange stays (q read, split records, combine, output rows, flags)
+//   2: also no split records, combine or output rows: per layer only the q
+//      read and the device-wide completion handoff
+//   3: the device-wide handoff alone
+//   4: the math on register contents, no K/V loads or LDS DMA
+//   5: the K/V loads and DMA, no math (each tile only waited for)
+#ifndef STEP_FLOOR
+#define STEP_FLOOR 0
+#endif
+constexpr int kFloor = STEP_FLOOR;
+
 // Id of the XCD (and so of the L2) this wave runs on.
 __device__ __forceinline__ uint32_t xcc_id() {
   uint32_t v;
@@ -365,7 +379,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       wave_lds_sync();
       const int32_t tiles = k1 > k0 ? (k1 - k0 + kTileKeys - 1) / kTileKeys : 0;
       target = gi;
-      slots = wave_uniform(max(0, min(kLdsSlots, tiles - kRegTiles)));
+      slots = (kFloor >= 1 && kFloor <= 4) ? 0
+                                           : wave_uniform(max(0, min(kLdsSlots, tiles - kRegTiles)));
       filled = 0;
     };
     auto request = [&](int count) {
@@ -502,7 +517,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
       // Layer i's inputs exist only now: q rows and appended K/V rows of the
       // unit, read device-coherently and staged in LDS for the compute waves.
-      {
+      if (kFloor < 3) {
         const int32_t qoff = (int32_t)((i * q_stride + (u * kSGroup + (lane >> 5)) * kSDim +
                                         (lane & 31) * kPackElems) * 2);
         const int32_t kvoff = (int32_t)((i * kv_stride + u * kSDim + (lane & 31) * kPackElems) * 2);
@@ -521,7 +536,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       // Combine unit u's splits for the 8-dim chunks c = split, split +
       // splits, ... of both rows: one round of L2 loads per chunk; the
       // chunk is emptied again right after it is read.
-      for (int32_t c = split; active && c < kChunks; c += p.splits) {
+      for (int32_t c = split; kFloor < 2 && active && c < kChunks; c += p.splits) {
         // Lanes past the live splits read split 0 and weigh it zero.
         const int32_t off = record(live ? sp : 0) + (c * kChunkFloats + g * kHalfChunk) * 4;
         struct Poll {
@@ -643,9 +658,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     const int32_t k0 = first + split * split_size;
     const int32_t k1 = active ? min(seq_len, k0 + split_size) : k0;
     const int32_t tiles = k1 > k0 ? (k1 - k0 + kTileKeys - 1) / kTileKeys : 0;
-    v.n_tiles = tiles > wave ? min((tiles - wave + kComputeWaves - 1) / kComputeWaves,
-                                   kWaveKeys / kTileKeys)
-                             : 0;
+    v.n_tiles = tiles > wave && (kFloor == 0 || kFloor >= 4)
+                    ? min((tiles - wave + kComputeWaves - 1) / kComputeWaves,
+                          kWaveKeys / kTileKeys)
+                    : 0;
     const bool live_new = new_pos >= first && new_pos < seq_len;
     const int32_t owner_split = live_new ? (new_pos - first) / max(split_size, 1) : 0;
     const int32_t owner_wave = live_new ? ((new_pos - k0) / kTileKeys) % kComputeWaves : 0;
@@ -662,7 +678,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     v.lds = kind == 1;
     v.par = slot;
     v.kind = kind;
-    v.new_row = wave_uniform(new_row);
+    v.new_row = (kFloor >= 1 && kFloor <= 3) ? -1 : wave_uniform(new_row);
     // Two table entries per lane: wave-local key e = lane, lane + 64.
     const int32_t *pt = p.page_table[kind] + b * c.max_pages_per_seq;
     int32_t rows[2];
@@ -701,8 +717,13 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     for (int kl = 0; kl < kTileLoads; ++kl) {
       tb.valid |= (rows[kl] >= 0 ? 1u : 0u) << kl;
       const int64_t off = (int64_t)(rows[kl] < 0 ? 0 : rows[kl]) * kRowElems + col;
-      tb.k[kl] = load128_stream(kb + off);
-      tb.v[kl] = load128_stream(vb + off);
+      if constexpr (kFloor == 4) {
+        tb.k[kl] = make_uint4(rows[kl], lane, kl, t);
+        tb.v[kl] = make_uint4(t, kl, lane, rows[kl]);
+      } else {
+        tb.k[kl] = load128_stream(kb + off);
+        tb.v[kl] = load128_stream(vb + off);
+      }
     }
   };
 
@@ -793,6 +814,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     }
   };
   auto compute = [&](const TileBuf &t) {
+    if constexpr (kFloor == 5) {
+#pragma unroll
+      for (int kl = 0; kl < kTileLoads; ++kl) {
+        asm volatile("" ::"v"(t.k[kl].x), "v"(t.k[kl].y), "v"(t.k[kl].z), "v"(t.k[kl].w));
+        asm volatile("" ::"v"(t.v[kl].x), "v"(t.v[kl].y), "v"(t.v[kl].z), "v"(t.v[kl].w));
+      }
+      return;
+    }
     scores(t.k, t.valid);
     accumulate(t.v, t.valid);
   };
@@ -885,6 +914,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
 #pragma unroll
         for (int kl = 0; kl < kTileLoads; ++kl) kv[kl] = s_tiles[(slot * 8 + kl) * kWave + lane];
         if (has_new) patch_packs(kv, valid_k, view, 0);
+        if constexpr (kFloor == 5) {
+#pragma unroll
+          for (int kl = 0; kl < kTileLoads; ++kl)
+            asm volatile("" ::"v"(kv[kl].x), "v"(kv[kl].y), "v"(kv[kl].z), "v"(kv[kl].w));
+          continue;
+        }
         scores(kv, valid_k);
 #pragma unroll
         for (int kl = 0; kl < kTileLoads; ++kl) kv[kl] = s_tiles[(slot * 8 + 4 + kl) * kWave + lane];
@@ -934,7 +969,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     }
     STEP_MARK(4);
     step_barrier();  // B
-    if (active) {
+    if (kFloor < 2 && active) {
       float big_m = -INFINITY;
 #pragma unroll
       for (int w = 0; w < kComputeWaves; ++w) big_m = fmaxf(big_m, s_ml[w][rec_g][0]);
