@@ -109,6 +109,7 @@ constexpr int kRecordFloats = kChunks * kChunkFloats;
 constexpr int kXcds = 8;                      // XCDs of an MI355X
 constexpr int kXcdSlots = 32;                 // workgroups (CUs) per XCD
 constexpr int kMaxBatch = 8;                  // at least 4 splits per unit
+constexpr int32_t kMaxWalkSteps = 0xffff;     // iterations of one walk (flag stamps)
 constexpr uint32_t kSentinel = 0x7fa5a5a5u;   // signalling NaN
 constexpr int kHeaderInts = 64;               // epoch, error, ..., pad
 // Header words: launch epoch; error code (0 ok, 1 a wait gave up, 2 a split
@@ -154,6 +155,7 @@ struct StepParams {
   int32_t batch;
   int32_t first_layer;
   int32_t layer_count;
+  int32_t walk_layer;     // walks: the cache layer every iteration uses
   int32_t units;
   int32_t splits;
   float q_scale;
@@ -186,7 +188,7 @@ __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memr
 #if STEP_TRACE
 #define STEP_MARK(e)                                                                     \
   do {                                                                                   \
-    if (lane == 0 && (wave == kControlWave || wave == 0))                                \
+    if (lane == 0 && (wave == kControlWave || wave == 0) && i < kNumModelLayers)        \
       p.trace[((int64_t)(xcd * kXcdSlots + ticket) * kNumModelLayers + i) * 10 + (e)] = \
           now_ticks();                                                                   \
   } while (0)
@@ -264,6 +266,13 @@ struct LayerView {
   int par;                // row table: s_rows[par]
 };
 
+// kWalk = false: iteration i is model layer first_layer + i of one decode
+// step (the sliding or global cache by the model's layer cadence).
+// kWalk = true: iteration i is decode step i of one layer (cache layer
+// walk_layer of cache 0): the sequences' lengths grow by one per iteration
+// and each iteration appends its token before attending, so later
+// iterations read rows that other workgroups appended in this launch.
+template <bool kWalk>
 __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p) {
   __shared__ int4 s_rows[2][kComputeWaves][kWaveKeys / 4];  // [layer parity][wave]
   __shared__ float s_prob[kComputeWaves][kWave];
@@ -308,8 +317,13 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   const int32_t split = active ? ticket / p.batch : p.splits;  // inactive: no keys
   const int32_t head = xcd;
   const int32_t u = b * kSHeads + head;
-  const int32_t seq_len = wave_uniform(p.seq_lengths[b]);
-  const int32_t new_pos = wave_uniform(p.token_position[b]);
+  // Step: the lengths and token positions as prepared for this step. Walk:
+  // the lengths before the walk; iteration i appends position len + i and
+  // attends over len + i + 1 keys.
+  const int32_t seq_len = wave_uniform(kWalk ? p.seq_lengths[b] + 1 : p.seq_lengths[b]);
+  const int32_t new_pos = wave_uniform(kWalk ? p.seq_lengths[b] : p.token_position[b]);
+  auto seq_at = [&](int32_t i) { return kWalk ? seq_len + i : seq_len; };
+  auto pos_at = [&](int32_t i) { return kWalk ? new_pos + i : new_pos; };
   const int64_t q_stride = (int64_t)p.units * kSGroup * kSDim;  // per layer
   const int64_t kv_stride = (int64_t)p.units * kSDim;
   // Split records: one buffer over the whole region, addressed in bytes.
@@ -318,7 +332,15 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     return (u * p.splits + s) * (kRecordFloats * 4);
   };
   const int32_t epoch = wave_uniform(s_epoch);
-  auto is_global_i = [&](int32_t i) { return model_layer_global(p.first_layer + i); };
+  auto is_global_i = [&](int32_t i) { return !kWalk && model_layer_global(p.first_layer + i); };
+  // Flag words of iteration i and the value that marks it complete. A step
+  // uses one flag row per model layer and marks it with the launch epoch; a
+  // walk cycles four rows and marks iteration i with (epoch, i) in one word
+  // (an iteration's row is rewritten only after every workgroup is past it).
+  auto fslot = [&](int32_t i) { return kWalk ? (i & 3) : i; };
+  auto stamp = [&](int32_t i) {
+    return kWalk ? (int32_t)(((uint32_t)epoch << 16) | ((uint32_t)i & 0xffffu)) : epoch;
+  };
   // Zeros for the output chunks this workgroup owns (those it combines:
   // c = split, split + splits, ... of both rows of unit u), layers from..end.
   auto zero_own_chunks = [&](int32_t from) {
@@ -440,24 +462,25 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
     };
     // A split longer than the row tables hold would drop keys: report it.
-    for (int kind = 0; kind < 2; ++kind) {
+    for (int kind = 0; kind < (kWalk ? 1 : 2); ++kind) {
       const Gemma4KvCacheConfig &c = p.c[kind];
-      int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;
+      const int32_t last_len = seq_at(p.layer_count - 1);  // the longest iteration
+      int32_t first = c.window_size > 0 ? last_len - c.window_size : 0;
       first = first < 0 ? 0 : first;
-      const int32_t n_keys = seq_len > first ? seq_len - first : 0;
+      const int32_t n_keys = last_len > first ? last_len - first : 0;
       if ((n_keys + p.splits - 1) / p.splits > kMaxSplitKeys) fail(2);
     }
     // Fault injection for tests: at layer stall_layer - 1, ticket 0 of XCD 0
     // waits, with the given limit, for a header word the host never sets.
     const int32_t stall_layer = wave_uniform(s_stall_layer);
     const uint64_t stall_ticks = (uint32_t)wave_uniform(s_stall_ticks);
-    // Polls a flag word per lane until every lane reads `epoch`, one load
+    // Polls a flag word per lane until every lane reads `want`, one load
     // in flight at a time (keeping up to four in flight measured no faster:
     // the flag's propagation, not the poll spacing, sets the wait).
-    auto poll = [&](auto load) {
+    auto poll = [&](int32_t want, auto load) {
       const uint64_t t0 = now_ticks();
       while (!abort) {
-        if (__ballot(load() != epoch) == 0) return;
+        if (__ballot(load() != want) == 0) return;
         if (now_ticks() - t0 > kWaitTicks) fail(1);
       }
     };
@@ -465,8 +488,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     const BufferRsrc flag_buf =
         buffer_of(p.global_flags, (int64_t)kNumModelLayers * kGlobalFlagStride * 4);
     auto wait_layer_device = [&](int32_t layer_i) {
-      const int32_t off = (layer_i * kGlobalFlagStride + (lane & (kXcds - 1))) * 4;
-      poll([&] {
+      const int32_t off = (fslot(layer_i) * kGlobalFlagStride + (lane & (kXcds - 1))) * 4;
+      poll(stamp(layer_i), [&] {
         return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(flag_buf, off, 0, kCoherentAux);
       });
     };
@@ -475,13 +498,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     // trip, so they start together).
     const BufferRsrc go_buf = buffer_of(p.go_flags, (int64_t)kNumModelLayers * kXcds * 16 * 4);
     auto wait_layer = [&](int32_t layer_i) {
-      const int32_t off = ((layer_i * kXcds + xcd) * 16) * 4;
+      const int32_t off = ((fslot(layer_i) * kXcds + xcd) * 16) * 4;
       if (ticket == 0) {
         wait_layer_device(layer_i);
-        if (lane == 0) __builtin_amdgcn_raw_buffer_store_b32((uint32_t)epoch, go_buf, off, 0, 0);
+        if (lane == 0)
+          __builtin_amdgcn_raw_buffer_store_b32((uint32_t)stamp(layer_i), go_buf, off, 0, 0);
         return;
       }
-      poll([&] {
+      poll(stamp(layer_i), [&] {
         return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(go_buf, off, 0, kLocalLoadAux);
       });
     };
@@ -490,11 +514,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     const BufferRsrc local_buf =
         buffer_of(p.local_flags, (int64_t)kNumModelLayers * kXcds * kXcdSlots * 4);
     auto publish_xcd = [&](int32_t layer_i) {
-      const int32_t off = ((layer_i * kXcds + xcd) * kXcdSlots + (lane & (kXcdSlots - 1))) * 4;
-      poll([&] {
+      const int32_t off =
+          ((fslot(layer_i) * kXcds + xcd) * kXcdSlots + (lane & (kXcdSlots - 1))) * 4;
+      poll(stamp(layer_i), [&] {
         return (int32_t)__builtin_amdgcn_raw_buffer_load_b32(local_buf, off, 0, kLocalLoadAux);
       });
-      if (lane == 0) coherent_store_i32(p.global_flags + layer_i * kGlobalFlagStride + xcd, epoch);
+      if (lane == 0)
+        coherent_store_i32(p.global_flags + fslot(layer_i) * kGlobalFlagStride + xcd,
+                           stamp(layer_i));
     };
     // Lane (g, sp) = (lane / 32, lane % 32) reads split sp's row g, so the
     // reductions over splits stay within 32-lane halves (DPP row ops and
@@ -618,8 +645,9 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       // My output slices and chunk resets are complete before my local flag.
       wait_stores_complete();
       if (lane == 0) {
-        __builtin_amdgcn_raw_buffer_store_b32((uint32_t)epoch, local_buf,
-                                              ((i * kXcds + xcd) * kXcdSlots + ticket) * 4, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(
+            (uint32_t)stamp(i), local_buf, ((fslot(i) * kXcds + xcd) * kXcdSlots + ticket) * 4,
+            0, 0);
       }
       if (ticket == 0) publish_xcd(i);
       STEP_MARK(7);
@@ -628,6 +656,13 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       // Every workgroup has read the header (and finished): advance it.
       wait_layer(p.layer_count - 1);
       if (lane == 0) coherent_store_i32(p.header + kHeaderEpoch, epoch);
+      if (kWalk && !abort && lane < p.batch) {
+        // Every workgroup read the lengths at entry: leave the metadata of
+        // the walk's last step (as a decode step's preparation would).
+        const int32_t last = p.seq_lengths[lane] + p.layer_count - 1;
+        const_cast<int32_t *>(p.seq_lengths)[lane] = last + 1;
+        const_cast<int32_t *>(p.token_position)[lane] = last;
+      }
     }
     // This wave gave up a wait: its chunks of the layers before that are
     // zeroed too, so none of its output is left from a failed step.
@@ -648,9 +683,10 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   auto setup = [&](int32_t i, int slot) -> LayerView {
     LayerView v;
     const int32_t layer = p.first_layer + i;
-    const int kind = model_layer_global(layer) ? 1 : 0;
+    const int kind = !kWalk && model_layer_global(layer) ? 1 : 0;
     const Gemma4KvCacheConfig &c = p.c[kind];
-    const int32_t cache_layer = wave_uniform(cache_layer_of(layer));
+    const int32_t cache_layer = kWalk ? p.walk_layer : wave_uniform(cache_layer_of(layer));
+    const int32_t seq_len = seq_at(i), new_pos = pos_at(i);
     int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;
     first = first < 0 ? 0 : first;
     const int32_t n_keys = seq_len > first ? seq_len - first : 0;
@@ -707,6 +743,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     uint32_t valid;
   };
   const int32_t col = head * kSDim + cpack * kPackElems;  // element offset in a cache row
+  // Walks: the cache as buffers (the host keeps it under 2 GiB).
+  const int64_t walk_bytes = (int64_t)p.c[0].num_layers * p.c[0].num_pages * p.c[0].page_size *
+                             kRowElems * 2;
+  const BufferRsrc walk_k = buffer_of(p.cache_k[0], walk_bytes);
+  const BufferRsrc walk_v = buffer_of(p.cache_v[0], walk_bytes);
   auto issue = [&](TileBuf &tb, const LayerView &v, int t) {
     const int4 rr = s_rows[v.par][wave][t * 2 + r];
     const int32_t rows[4] = {rr.x, rr.y, rr.z, rr.w};
@@ -720,6 +761,15 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       if constexpr (kFloor == 4) {
         tb.k[kl] = make_uint4(rows[kl], lane, kl, t);
         tb.v[kl] = make_uint4(t, kl, lane, rows[kl]);
+      } else if constexpr (kWalk) {
+        // Rows appended earlier in this launch were written by other
+        // workgroups of this XCD: sc0|nt loads skip this CU's L1 (which may
+        // still hold the slot's previous row) and read the shared L2.
+        const int32_t boff = (int32_t)(off * 2);
+        const u32x4 kk = __builtin_amdgcn_raw_buffer_load_b128(walk_k, boff, 0, kLocalLoadAux);
+        const u32x4 vv = __builtin_amdgcn_raw_buffer_load_b128(walk_v, boff, 0, kLocalLoadAux);
+        tb.k[kl] = make_uint4(kk[0], kk[1], kk[2], kk[3]);
+        tb.v[kl] = make_uint4(vv[0], vv[1], vv[2], vv[3]);
       } else {
         tb.k[kl] = load128_stream(kb + off);
         tb.v[kl] = load128_stream(vb + off);
@@ -852,6 +902,14 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   // layer i+1 are requested. (Issuing them earlier -- several layers ahead
   // for a global layer, or two layers ahead for sliding ones -- was measured
   // slower: the waits of the layers in between then cover those loads too.)
+  auto append_new = [&](const LayerView &v) {
+    if (v.new_row >= 0 && r == 0) {
+      const int64_t dst = (int64_t)v.new_row * kRowElems + col;
+      store128(p.cache_k[v.kind] + dst, s_new[cpack]);
+      store128(p.cache_v[v.kind] + dst, s_new[kLPR + cpack]);
+    }
+  };
+
   TileBuf buf[kPrefetchTiles];
   LayerView cur;
   auto prepare = [&](int32_t i) {  // at the end of layer i (i = -1: start)
@@ -876,6 +934,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     step_barrier();  // A: layer i-1 published (or i == 0), inputs in LDS
     STEP_MARK(3);
     const LayerView view = cur;
+    // A walk appends first, so the store has landed long before barrier B.
+    if constexpr (kWalk) append_new(view);
 #pragma unroll
     for (int g = 0; g < kSGroup; ++g) {
       const uint4 qp = s_q[g * kLPR + cpack];
@@ -938,10 +998,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         }
       }
     }
-    if (view.new_row >= 0 && r == 0) {
-      const int64_t dst = (int64_t)view.new_row * kRowElems + col;
-      store128(p.cache_k[view.kind] + dst, s_new[cpack]);
-      store128(p.cache_v[view.kind] + dst, s_new[kLPR + cpack]);
+    if constexpr (!kWalk) {
+      append_new(view);
+    } else if (view.new_row >= 0) {
+      // The appended row is in the L2 before this split's record, so every
+      // split that reads it next iteration (after the records) sees it.
+      wait_stores_complete();
     }
 
     // Wave totals to LDS, then the compute waves' partials are merged.
@@ -1088,15 +1150,15 @@ StepParams base_params(void *workspace, const WorkspaceLayout &w, int32_t batch_
 // workspace header; nothing hangs.
 std::atomic<int> g_cooperative{0};
 
-hipError_t launch_step(StepParams &p, hipStream_t stream) {
+hipError_t launch_step(StepParams &p, hipStream_t stream, bool walk = false) {
   void *args[] = {&p};
+  const void *fn = walk ? reinterpret_cast<const void *>(decode_step_kernel<true>)
+                        : reinterpret_cast<const void *>(decode_step_kernel<false>);
   if (p.probe == nullptr && g_cooperative.load(std::memory_order_relaxed) != 0) {
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void *>(decode_step_kernel),
-                                      dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds,
-                                      stream);
+    return hipLaunchCooperativeKernel(fn, dim3(kStepWorkgroups), dim3(kStepThreads), args,
+                                      kPadLds, stream);
   }
-  return hipLaunchKernel(reinterpret_cast<const void *>(decode_step_kernel),
-                         dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds, stream);
+  return hipLaunchKernel(fn, dim3(kStepWorkgroups), dim3(kStepThreads), args, kPadLds, stream);
 }
 
 __global__ void decode_step_set_stall_kernel(int32_t *header, int32_t stall_layer_plus1,
@@ -1137,9 +1199,11 @@ extern "C" hipError_t gemma4_decode_step_workspace_init(void *workspace, size_t 
   if (e != hipSuccess) return e;
   if (device < 0 || device >= 64) return hipErrorNotSupported;
   if (g_placement_ok[device].load() == 0) {
-    e = hipFuncSetAttribute(reinterpret_cast<const void *>(decode_step_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPadLds);
-    if (e != hipSuccess) return e;
+    for (const void *fn : {reinterpret_cast<const void *>(decode_step_kernel<false>),
+                           reinterpret_cast<const void *>(decode_step_kernel<true>)}) {
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kPadLds);
+      if (e != hipSuccess) return e;
+    }
     // One probe launch of the step kernel: every XCD must receive exactly
     // 32 of its workgroups, on 32 distinct CUs, for the XCD-local exchange.
     StepParams p = base_params(workspace, w, batch_count);
@@ -1370,4 +1434,54 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
     l += run;
   }
   return hipSuccess;
+}
+
+extern "C" hipError_t gemma4_decode_walk_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *cache_k, gemma4_bf16 *cache_v, const int32_t *page_table,
+    Gemma4KvCacheConfig config, int32_t layer, int32_t *seq_lengths, int32_t *token_position,
+    int32_t steps, float scale, int32_t batch_count, void *workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+  const size_t need = gemma4_decode_step_workspace_bytes(batch_count);
+  if (out == nullptr || q == nullptr || k == nullptr || v == nullptr || cache_k == nullptr ||
+      cache_v == nullptr || page_table == nullptr || seq_lengths == nullptr ||
+      token_position == nullptr || workspace == nullptr || need == 0 ||
+      workspace_bytes < need || steps < 1 || steps > kMaxWalkSteps || !(scale > 0.0f) ||
+      !step_geometry_ok(config, batch_count) || layer < 0 || layer >= config.num_layers)
+    return hipErrorInvalidValue;
+  const WorkspaceLayout w = workspace_layout(batch_count);
+  // Every iteration's split must fit the row tables: the window, or the
+  // longest global range the cache can hold.
+  const int64_t live =
+      config.window_size > 0 ? config.window_size : (int64_t)config.max_pages_per_seq * config.page_size;
+  if ((live + w.splits - 1) / w.splits > kMaxSplitKeys) return hipErrorInvalidValue;
+  // The cache is read through buffer descriptors and the rows through
+  // 32-bit byte offsets.
+  const int64_t cache_bytes =
+      (int64_t)config.num_layers * config.num_pages * config.page_size * kRowElems * 2;
+  const int64_t io_bytes = (int64_t)steps * w.units * kSGroup * kSDim * 2;
+  if (cache_bytes >= ((int64_t)1 << 31) || io_bytes >= ((int64_t)1 << 31))
+    return hipErrorInvalidValue;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64 ||
+      g_placement_ok[device].load() != 1)
+    return hipErrorNotSupported;  // gemma4_decode_step_workspace_init first
+  StepParams p = base_params(workspace, w, batch_count);
+  p.out = reinterpret_cast<uint16_t *>(out);
+  p.q = reinterpret_cast<const uint16_t *>(q);
+  p.new_k = reinterpret_cast<const uint16_t *>(k);
+  p.new_v = reinterpret_cast<const uint16_t *>(v);
+  for (int kind = 0; kind < 2; ++kind) {
+    p.cache_k[kind] = reinterpret_cast<uint16_t *>(cache_k);
+    p.cache_v[kind] = reinterpret_cast<uint16_t *>(cache_v);
+    p.page_table[kind] = page_table;
+    p.c[kind] = config;
+  }
+  p.seq_lengths = seq_lengths;
+  p.token_position = token_position;
+  p.first_layer = 0;
+  p.layer_count = steps;
+  p.walk_layer = layer;
+  p.q_scale = scale * kLog2e;
+  return launch_step(p, stream, true);
 }

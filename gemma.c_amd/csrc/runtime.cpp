@@ -279,7 +279,66 @@ struct Gemma4Runtime {
   Gemma4RuntimeState state;
 };
 
+hipError_t gemma4_runtime_prepare_decode_walk(Gemma4RuntimeState *s, int32_t steps,
+                                              hipStream_t stream) {
+  if (s == nullptr || steps < 1) return hipErrorInvalidValue;
+  if (s->host_stale) {
+    const hipError_t se = gemma4_runtime_sync_host(s, stream);
+    if (se != hipSuccess) return se;
+  }
+  const Gemma4KvCacheConfig &sc = s->sliding_cache_config;
+  const Gemma4KvCacheConfig &gc = s->global_cache_config;
+  // Every step of every sequence is mapped on copies first, so a refused
+  // walk leaves the state as it was (the per-step checks of
+  // gemma4_runtime_prepare_decode_step, applied to each position in order).
+  std::vector<int32_t> spt = s->h_sliding_page_table, sslot = s->h_sliding_slot_logical_pages;
+  std::vector<int32_t> gpt = s->h_global_page_table, gslot = s->h_global_slot_logical_pages;
+  std::vector<int32_t> before(s->h_seq_lengths.begin(), s->h_seq_lengths.begin() + s->batch_size);
+  for (int32_t b = 0; b < s->batch_size; ++b) {
+    const int32_t pos0 = before[b];
+    if (pos0 < 0 || (int64_t)pos0 + steps > s->max_seq_len) return hipErrorInvalidValue;
+    for (int32_t t = 0; t < steps; ++t) {
+      if (gemma4_kv_cache_ensure_page(spt, sslot, sc, b, pos0 + t) < 0 ||
+          gemma4_kv_cache_ensure_page(gpt, gslot, gc, b, pos0 + t) < 0)
+        return hipErrorInvalidValue;
+    }
+  }
+  s->h_sliding_page_table.swap(spt);
+  s->h_sliding_slot_logical_pages.swap(sslot);
+  s->h_global_page_table.swap(gpt);
+  s->h_global_slot_logical_pages.swap(gslot);
+  for (int32_t b = 0; b < s->batch_size; ++b) {
+    s->h_token_batch[b] = b;
+    s->h_token_position[b] = before[b] + steps - 1;
+    s->h_seq_lengths[b] = before[b] + steps;
+  }
+  s->token_count = s->batch_size;
+  hipError_t e = upload(s->sliding_page_table, s->h_sliding_page_table.data(),
+                        s->h_sliding_page_table.size(), stream);
+  if (e == hipSuccess)
+    e = upload(s->global_page_table, s->h_global_page_table.data(), s->h_global_page_table.size(),
+               stream);
+  if (e == hipSuccess)
+    e = upload(s->sliding_slot_logical_pages, s->h_sliding_slot_logical_pages.data(),
+               s->h_sliding_slot_logical_pages.size(), stream);
+  if (e == hipSuccess)
+    e = upload(s->global_slot_logical_pages, s->h_global_slot_logical_pages.data(),
+               s->h_global_slot_logical_pages.size(), stream);
+  if (e == hipSuccess)
+    e = upload(s->token_batch, s->h_token_batch.data(), (size_t)s->batch_size, stream);
+  // The device lengths stay at their values before the walk, which is what
+  // the walk reads (it leaves the last step's lengths and positions).
+  if (e == hipSuccess) e = upload(s->seq_lengths, before.data(), before.size(), stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);  // `before` is a local
+  return e;
+}
+
 extern "C" {
+
+hipError_t gemma4_runtime_decode_walk(Gemma4Runtime *rt, int32_t steps, hipStream_t stream) {
+  return rt == nullptr ? hipErrorInvalidValue
+                       : gemma4_runtime_prepare_decode_walk(&rt->state, steps, stream);
+}
 
 hipError_t gemma4_runtime_create(Gemma4Runtime **out, int32_t batch_size, int32_t max_seq_len,
                                  int32_t page_size, hipStream_t stream) {

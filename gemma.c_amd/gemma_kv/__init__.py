@@ -114,6 +114,9 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_decode_step_inject_stall": (_I32, [_P, _I32, ctypes.c_uint32, _P]),
     "gemma4_decode_step_set_cooperative": (_I32, [_I32]),
+    "gemma4_decode_walk_bf16": (
+        _I32, [_P] * 7 + [_CFG, _I32, _P, _P, _I32, _F32, _I32, _P, ctypes.c_size_t, _P]),
+    "gemma4_runtime_decode_walk": (_I32, [_P, _I32, _P]),
     "gemma4_decode_step_layers_bf16": (
         _I32, [_P, _P, _P, _P, _P, _P, _P, _CFG, _P, _P, _P, _CFG, _P, _P, _I32, _I32, _F32,
                _I32, _P, ctypes.c_size_t, _P]),
@@ -335,6 +338,15 @@ def decode_step_layers_bf16(out, q, k, v, sliding_k, sliding_v, sliding_page_tab
         workspace.numel() * workspace.element_size(), stream_handle(stream))
 
 
+def decode_walk_bf16(out, q, k, v, cache_k, cache_v, page_table, config, layer,
+                     seq_lengths, token_position, steps, softmax_scale, batch_count,
+                     workspace, stream=None) -> int:
+    return lib().gemma4_decode_walk_bf16(
+        ptr(out), ptr(q), ptr(k), ptr(v), ptr(cache_k), ptr(cache_v), ptr(page_table), config,
+        layer, ptr(seq_lengths), ptr(token_position), steps, softmax_scale, batch_count,
+        ptr(workspace), workspace.numel() * workspace.element_size(), stream_handle(stream))
+
+
 class Runtime:
     """Owner of a Gemma4RuntimeState (caches, page tables, token metadata),
     mirroring src/gemma4_runtime.cuh through the opaque-handle C-ABI."""
@@ -372,6 +384,9 @@ class Runtime:
 
     def prepare_decode_step_device(self, stream=None) -> int:
         return lib().gemma4_runtime_decode_step_device(self._h, stream_handle(stream))
+
+    def prepare_decode_walk(self, steps, stream=None) -> int:
+        return lib().gemma4_runtime_decode_walk(self._h, steps, stream_handle(stream))
 
     def sync_host(self, stream=None) -> int:
         return lib().gemma4_runtime_sync_host_state(self._h, stream_handle(stream))

@@ -306,6 +306,31 @@ hipError_t gemma4_decode_step_layers_bf16(
     int32_t layer_count, float scale, int32_t batch_count, void *workspace,
     size_t workspace_bytes, hipStream_t stream);
 
+// ---- persistent walk over decode steps of one layer ----------------------
+// `steps` consecutive decode steps of one 8 x 256 cache layer in one
+// persistent launch (the same kernel, placement and workspace as the step
+// above): step s appends token s of every sequence at position
+// seq_lengths[b] + s and attends over its seq_lengths[b] + s + 1 keys, the
+// window's last ones for a sliding cache. This is the reference's per-step
+// loop for one layer (src/gemma4_decode_megakernel.cu:172-183 preparing
+// each step with gemma4_runtime_prepare_decode_step,
+// src/gemma4_runtime.cu:276-341) without a launch per step; step s reads its
+// q/k/v only after step s-1's output is complete.
+//   q, out: [steps][batch_count][16][256]; k, v: [steps][batch_count][8][256].
+//   seq_lengths: device lengths before the walk (the runtime's current
+//   ones); the page table must map every position the walk appends
+//   (gemma4_runtime_prepare_decode_walk does both). On completion, in stream
+//   order, seq_lengths and token_position hold the last step's values, as
+//   after that many gemma4_runtime_prepare_decode_step calls.
+// steps <= 65535; cache (one of K/V) and q under 2 GiB. Workspace, status and
+// failure semantics as for gemma4_decode_step_layers_bf16.
+hipError_t gemma4_decode_walk_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *cache_k, gemma4_bf16 *cache_v, const int32_t *page_table,
+    Gemma4KvCacheConfig config, int32_t layer, int32_t *seq_lengths, int32_t *token_position,
+    int32_t steps, float scale, int32_t batch_count, void *workspace, size_t workspace_bytes,
+    hipStream_t stream);
+
 #ifdef __cplusplus
 }  // extern "C"
 #endif

@@ -80,6 +80,16 @@ hipError_t gemma4_runtime_prepare_decode_step(Gemma4RuntimeState *state,
 // first by themselves).
 hipError_t gemma4_runtime_prepare_decode_step_device(Gemma4RuntimeState *state,
                                                      hipStream_t stream);
+// Metadata for a persistent walk of `steps` decode steps
+// (gemma4_decode_walk_bf16; no counterpart in the reference, whose loop
+// prepares one step at a time with gemma4_runtime_prepare_decode_step):
+// validates every step of every sequence before mutating anything, maps the
+// ring slots of all `steps` positions, uploads the page tables, and leaves
+// the host vectors as after the last step. The device seq_lengths hold the
+// lengths before the walk, which the walk advances itself; run the walk next
+// in the same stream. Synchronises `stream` once.
+hipError_t gemma4_runtime_prepare_decode_walk(Gemma4RuntimeState *state, int32_t steps,
+                                              hipStream_t stream);
 // Copies the device metadata into the host vectors (synchronous).
 hipError_t gemma4_runtime_sync_host(Gemma4RuntimeState *state, hipStream_t stream);
 // Status of the last device-side step (synchronous read): 0 applied, 1 refused.
@@ -101,6 +111,7 @@ hipError_t gemma4_runtime_decode_step(Gemma4Runtime *rt, hipStream_t stream);
 // Handle forms of the device-side step, the host sync and the status read
 // (no counterparts in the reference; see the C++ functions above).
 hipError_t gemma4_runtime_decode_step_device(Gemma4Runtime *rt, hipStream_t stream);
+hipError_t gemma4_runtime_decode_walk(Gemma4Runtime *rt, int32_t steps, hipStream_t stream);
 hipError_t gemma4_runtime_sync_host_state(Gemma4Runtime *rt, hipStream_t stream);
 hipError_t gemma4_runtime_get_device_step_status(const Gemma4Runtime *rt, int32_t *status);
 // which: 0 sliding config, 1 global config.
