@@ -278,6 +278,36 @@ def bench_step_ref_geometry(torch, gk, dev, layers, caches, meta, steps):
                       "global launches per step"}
 
 
+def bench_step_prep(torch, gk, runner, steps):
+    """Config 2 from the layers' raw projections
+    (gemma4_decode_step_layers_prep_bf16): the same persistent step with each
+    layer's Q/K RMSNorm + RoPE and V RMSNorm done in-kernel after the previous
+    layer completes, as the reference's fused decode layer does."""
+    dev = runner.q.device
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(12)
+    w = (1.0 + 0.1 * torch.randn((2, NUM_LAYERS, DIM), generator=gen, device=dev)).bfloat16()
+    w = w.view(torch.int16)
+    npos = CONTEXT + 1
+    ang = torch.rand((2, 2, npos, DIM // 2), generator=gen, device=dev) * 6.28
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    c, m = runner.caches, runner.meta
+
+    def fn(st):
+        gk.check(gk.decode_step_layers_prep_bf16(
+            runner.out, runner.q, runner.k, runner.v, c["sk"], c["sv"], m["s_pt"], runner.s_cfg,
+            c["gk"], c["gv"], m["g_pt"], runner.g_cfg, m["seq"], m["pos"], w[0], w[1],
+            cos[0, 0], sin[0, 0], cos[1, 0], sin[1, 0], 0, NUM_LAYERS, 1.0 / math.sqrt(DIM), 1,
+            runner.ws, stream=st), "decode_step_layers_prep")
+
+    warm_clock(torch, fn, 0.2)
+    ms = time_eager(torch, fn, steps, 3)
+    assert runner.status() == 0
+    return {"workload": "config2 from raw projections (in-step Q/K norm+RoPE, V norm)",
+            "ms_per_step": round(ms, 4), "us_per_layer_step": round(ms * 1e3 / NUM_LAYERS, 3),
+            "timing": "eager back-to-back steps, one persistent launch each"}
+
+
 def bench_prefill(torch, gk, dev, reps):
     """a 2048-row prefill chunk on one sliding layer (window
     1024, 1024-slot page-1 ring after a 1536-token prior) and one global layer
@@ -1078,6 +1108,7 @@ def main():
                      "single_launch_us_median": round(ms_single * 1e3, 2),
                      "algorithmic_bytes_per_launch": step_bytes},
     }
+    result["step_with_prep"] = bench_step_prep(torch, gk, runner, max(10, args.steps // 2))
     result["step_reference_global_geometry"] = bench_step_ref_geometry(
         torch, gk, dev, layers, caches, meta, max(10, args.steps // 2))
     if not args.no_batch64:

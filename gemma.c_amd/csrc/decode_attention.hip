@@ -970,12 +970,14 @@ hipError_t decode_append_gated(uint16_t *out, float *pm, float *pl, float *pacc,
                                const uint16_t *new_v, const Gemma4KvCacheConfig &c,
                                int32_t layer, float softmax_scale, int32_t split_size,
                                int32_t num_splits, int32_t batch_count, const int32_t *gate,
-                               hipStream_t stream) {
+                               hipStream_t stream, const uint16_t *q_norm_weight,
+                               const uint16_t *k_norm_weight, const float *cos,
+                               const float *sin) {
   if (token_position == nullptr || new_k == nullptr || gate == nullptr) return hipErrorInvalidValue;
   return decode_entry(out, pm, pl, pacc, q, cache_k, cache_v, page_table, seq_lengths,
                       token_position, new_k, new_v, nullptr, c, layer, softmax_scale, split_size,
-                      num_splits, batch_count, /*combine=*/true, stream, nullptr, nullptr, nullptr,
-                      nullptr, gate);
+                      num_splits, batch_count, /*combine=*/true, stream, q_norm_weight,
+                      k_norm_weight, cos, sin, gate);
 }
 
 }  // namespace gemma4

@@ -200,6 +200,8 @@ hipError_t decode_append_gated(uint16_t *out, float *pm, float *pl, float *pacc,
                                const uint16_t *new_v, const Gemma4KvCacheConfig &c,
                                int32_t layer, float softmax_scale, int32_t split_size,
                                int32_t num_splits, int32_t batch_count, const int32_t *gate,
-                               hipStream_t stream);
+                               hipStream_t stream, const uint16_t *q_norm_weight = nullptr,
+                               const uint16_t *k_norm_weight = nullptr,
+                               const float *cos = nullptr, const float *sin = nullptr);
 
 }  // namespace gemma4

@@ -67,6 +67,7 @@
 // touches no cache and exits, until the workspace is initialised again.
 #include "gemma4_device.hpp"
 #include "decode_common.hpp"
+#include "prep_common.hpp"
 
 #include "gemma4_flash_attention.h"
 
@@ -144,6 +145,14 @@ struct StepParams {
   Gemma4KvCacheConfig c[2];
   const int32_t *seq_lengths;
   const int32_t *token_position;
+  // Optional preparation of the layers' raw projections (all null: q/k/v
+  // are already prepared): learned RMSNorm weights per launch layer
+  // [layer_count][256] for Q and K, and RoPE tables [position][128] per cache
+  // kind ([0] sliding, [1] global).
+  const uint16_t *q_norm_w;
+  const uint16_t *k_norm_w;
+  const float *rope_cos[2];
+  const float *rope_sin[2];
   int32_t *header;
   uint32_t *tickets;      // [xcd * kTicketStride]
   int32_t *local_flags;   // [layer][xcd][slot]
@@ -207,10 +216,13 @@ __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memr
 //   3: the device-wide handoff alone
 //   4: the math on register contents, no K/V loads or LDS DMA
 //   5: the K/V loads and DMA, no math (each tile only waited for)
+//   6: every XCD's global-layer reads go to KV head 0's columns (results
+//      wrong; prices eight XCDs streaming the same bytes)
 #ifndef STEP_FLOOR
 #define STEP_FLOOR 0
 #endif
 constexpr int kFloor = STEP_FLOOR;
+
 
 // Id of the XCD (and so of the L2) this wave runs on.
 __device__ __forceinline__ uint32_t xcc_id() {
@@ -251,6 +263,49 @@ __device__ __forceinline__ BufferRsrc buffer_of(const void *base, int64_t bytes)
 __device__ __forceinline__ void local_store2(BufferRsrc r, int32_t off, float a, float b) {
   const u32x2 v = {__float_as_uint(a), __float_as_uint(b)};
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
+}
+
+// Preparation of one 256-dim row held by a 32-lane half, lane c owning dims
+// [8c, 8c + 8): RMSNorm, then (weighted) the learned weight and split-half
+// RoPE over all 256 dims with the position's cos/sin row (c's dims and their
+// partners, 16 lanes away, share the table entries [8c mod 128, +8)).
+// The per-layer preparation's arithmetic with its own reduction order for
+// the sum of squares (src/gemma4_flash_attention_decode.cu:233-283).
+__device__ __forceinline__ uint4 prep_row(uint4 raw, uint4 weight, bool weighted,
+                                          const float (&cs)[kPackElems],
+                                          const float (&sn)[kPackElems], int c) {
+  float x[8];
+  unpack8(raw, x);
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss = fmaf(x[j], x[j], ss);
+  // Sum over the row's 32 lanes, all exchanges on the VALU (DPP row ops and
+  // a 16-lane row swap).
+  ss += lane_pair<1>(ss);
+  ss += lane_pair<2>(ss);
+  ss += lane_pair<4>(ss);
+  ss += lane_pair<8>(ss);
+  ss += xor_lane16(ss);
+  const float scale = 1.0f / sqrtf(ss / (float)kSDim + kRmsEps);
+  float w[8];
+  unpack8(weight, w);
+  float y[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = weighted ? x[j] * scale * w[j] : x[j] * scale;
+  float partner[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) partner[j] = xor_lane16(y[j]);
+  const float sign = c < 16 ? -1.0f : 1.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = weighted ? fmaf(sign * partner[j], sn[j], y[j] * cs[j]) : y[j];
+  // Round to bf16 (nearest even) with the hardware pair conversion.
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16x2_t pr = {(__bf16)y[2 * j], (__bf16)y[2 * j + 1]};
+    o[j] = __builtin_bit_cast(uint32_t, pr);
+  }
+  return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // Everything a compute wave needs about one layer of its split.
@@ -374,7 +429,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       return (int32_t)-1;
     };
     const int r = lane / kLPR;
-    const int64_t col = (int64_t)head * kSDim + (lane % kLPR) * kPackElems;
+    const int64_t col = (int64_t)(kFloor == 6 ? 0 : head) * kSDim + (lane % kLPR) * kPackElems;
     const uint16_t *kb = p.cache_k[1] + col;
     const uint16_t *vb = p.cache_v[1] + col;
     int32_t target = -1, slots = 0, filled = 0;
@@ -534,6 +589,29 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     const BufferRsrc in_buf_v = buffer_of(p.new_v, (int64_t)p.layer_count * kv_stride * 2);
     for (int32_t i = 0; i < p.layer_count; ++i) {
       STEP_MARK(0);
+      // What the preparation needs besides the projections does not depend
+      // on the previous layer: this layer's norm weights and the RoPE row of
+      // the token's position are requested before the wait.
+      const bool prep = p.q_norm_w != nullptr;
+      uint4 w_q = make_uint4(0, 0, 0, 0), w_k = w_q;
+      float rc[kPackElems], rs[kPackElems];
+      if (prep) {
+        const int cp = lane & 31;
+        w_q = load128(p.q_norm_w + (int64_t)i * kSDim + cp * kPackElems);
+        w_k = load128(p.k_norm_w + (int64_t)i * kSDim + cp * kPackElems);
+        const int kind = is_global_i(i) ? 1 : 0;
+        const int32_t pos = max(pos_at(i), 0);
+        const int pair = (cp * kPackElems) % (kSDim / 2);
+        const float4 *cr = reinterpret_cast<const float4 *>(p.rope_cos[kind] +
+                                                             (int64_t)pos * (kSDim / 2) + pair);
+        const float4 *sr = reinterpret_cast<const float4 *>(p.rope_sin[kind] +
+                                                             (int64_t)pos * (kSDim / 2) + pair);
+        const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+        rc[0] = c0.x; rc[1] = c0.y; rc[2] = c0.z; rc[3] = c0.w;
+        rc[4] = c1.x; rc[5] = c1.y; rc[6] = c1.z; rc[7] = c1.w;
+        rs[0] = s0.x; rs[1] = s0.y; rs[2] = s0.z; rs[3] = s0.w;
+        rs[4] = s1.x; rs[5] = s1.y; rs[6] = s1.z; rs[7] = s1.w;
+      }
       if (i > 0) wait_layer(i - 1);
       STEP_MARK(1);
       if (i == stall_layer && xcd == 0 && ticket == 0) {
@@ -552,8 +630,16 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         const u32x4 nv = lane < 32
                              ? __builtin_amdgcn_raw_buffer_load_b128(in_buf_k, kvoff, 0, kCoherentAux)
                              : __builtin_amdgcn_raw_buffer_load_b128(in_buf_v, kvoff, 0, kCoherentAux);
-        s_q[lane] = make_uint4(qv[0], qv[1], qv[2], qv[3]);
-        s_new[lane] = make_uint4(nv[0], nv[1], nv[2], nv[3]);
+        uint4 qp = make_uint4(qv[0], qv[1], qv[2], qv[3]);
+        uint4 np = make_uint4(nv[0], nv[1], nv[2], nv[3]);
+        if (prep && pos_at(i) >= 0) {
+          // Q rows and the new K row: learned RMSNorm + RoPE; the new V row:
+          // scale-free RMSNorm (each row is one 32-lane half).
+          qp = prep_row(qp, w_q, true, rc, rs, lane & 31);
+          np = prep_row(np, w_k, lane < 32, rc, rs, lane & 31);
+        }
+        s_q[lane] = qp;
+        s_new[lane] = np;
       }
       STEP_MARK(2);
       step_barrier();  // A: layer i may start
@@ -751,8 +837,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   auto issue = [&](TileBuf &tb, const LayerView &v, int t) {
     const int4 rr = s_rows[v.par][wave][t * 2 + r];
     const int32_t rows[4] = {rr.x, rr.y, rr.z, rr.w};
-    const uint16_t *kb = p.cache_k[v.kind];
-    const uint16_t *vb = p.cache_v[v.kind];
+    const uint16_t *kb = p.cache_k[v.kind] - (kFloor == 6 && v.kind == 1 ? head * kSDim : 0);
+    const uint16_t *vb = p.cache_v[v.kind] - (kFloor == 6 && v.kind == 1 ? head * kSDim : 0);
     tb.valid = 0;
 #pragma unroll
     for (int kl = 0; kl < kTileLoads; ++kl) {
@@ -1267,6 +1353,16 @@ extern "C" hipError_t gemma4_decode_step_inject_stall(void *workspace, int32_t l
 namespace gemma4 {
 namespace {
 
+// Preparation inputs of a step (all null: q/k/v already prepared). Norm
+// weights: [layer_count][head_dim] of each layer's geometry, back to back;
+// RoPE tables per kind: [position][rotary_dim / 2].
+struct StepPrep {
+  const uint16_t *q_norm_w = nullptr;
+  const uint16_t *k_norm_w = nullptr;
+  const float *cos[2] = {nullptr, nullptr};
+  const float *sin[2] = {nullptr, nullptr};
+};
+
 // Whether the persistent kernel accepts model layers [first_layer,
 // first_layer + layer_count), all of them in 8 x 256 caches (no launch).
 hipError_t step_check(gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
@@ -1298,7 +1394,8 @@ hipError_t step_run(uint16_t *out, const uint16_t *q, const uint16_t *k, const u
                     const int32_t *const pt[2], const Gemma4KvCacheConfig cfg[2],
                     const int32_t *seq_lengths, const int32_t *token_position,
                     int32_t first_layer, int32_t layer_count, float scale,
-                    int32_t batch_count, void *workspace, hipStream_t stream) {
+                    int32_t batch_count, void *workspace, hipStream_t stream,
+                    const StepPrep &prep) {
   const hipError_t ok = step_check(ck, cv, pt, cfg, first_layer, layer_count, batch_count);
   if (ok != hipSuccess) return ok;
   const WorkspaceLayout w = workspace_layout(batch_count);
@@ -1318,13 +1415,23 @@ hipError_t step_run(uint16_t *out, const uint16_t *q, const uint16_t *k, const u
   p.first_layer = first_layer;
   p.layer_count = layer_count;
   p.q_scale = scale * kLog2e;
+  if (prep.q_norm_w != nullptr) {
+    p.q_norm_w = prep.q_norm_w;
+    p.k_norm_w = prep.k_norm_w;
+    for (int kind = 0; kind < 2; ++kind) {
+      p.rope_cos[kind] = prep.cos[kind];
+      p.rope_sin[kind] = prep.sin[kind];
+    }
+  }
   return launch_step(p, stream);
 }
 
 }  // namespace
 }  // namespace gemma4
 
-extern "C" hipError_t gemma4_decode_step_layers_bf16(
+namespace gemma4 {
+namespace {
+hipError_t step_layers(
     gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
     gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
     const int32_t *sliding_page_table, Gemma4KvCacheConfig sliding_config,
@@ -1332,7 +1439,7 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
     const int32_t *global_page_table, Gemma4KvCacheConfig global_config,
     const int32_t *seq_lengths, const int32_t *token_position, int32_t first_layer,
     int32_t layer_count, float scale, int32_t batch_count, void *workspace,
-    size_t workspace_bytes, hipStream_t stream) {
+    size_t workspace_bytes, hipStream_t stream, const StepPrep &prep) {
   const size_t need = gemma4_decode_step_workspace_bytes(batch_count);
   if (out == nullptr || q == nullptr || k == nullptr || v == nullptr || seq_lengths == nullptr ||
       token_position == nullptr || workspace == nullptr || need == 0 || workspace_bytes < need ||
@@ -1354,7 +1461,7 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
     return step_run(reinterpret_cast<uint16_t *>(out), reinterpret_cast<const uint16_t *>(q),
                     reinterpret_cast<const uint16_t *>(k), reinterpret_cast<const uint16_t *>(v),
                     ck, cv, pt, cfg, seq_lengths, token_position, first_layer, layer_count,
-                    scale, batch_count, workspace, stream);
+                    scale, batch_count, workspace, stream, prep);
   }
   // Reference global geometry: runs of sliding layers go to the persistent
   // kernel, each global layer to one fused append + split-K launch and the
@@ -1405,35 +1512,99 @@ extern "C" hipError_t gemma4_decode_step_layers_bf16(
   const uint16_t *kp = reinterpret_cast<const uint16_t *>(k);
   const uint16_t *vp = reinterpret_cast<const uint16_t *>(v);
   uint16_t *op = reinterpret_cast<uint16_t *>(out);
+  StepPrep lp = prep;  // norm weights advance with the layers
   for (int32_t l = first_layer; l < last;) {
     if (is_global(l)) {
       const int64_t slots = rows * ref_splits;
+      // With preparation the split kernel prepares q and the new K (V from
+      // the raw K, as the 1 x 512 geometry defines it).
       const hipError_t e = decode_append_gated(
           op, ref_partials, ref_partials + slots, ref_partials + 2 * slots, qp,
           reinterpret_cast<uint16_t *>(global_cache_k),
           reinterpret_cast<uint16_t *>(global_cache_v), global_page_table, seq_lengths,
-          token_position, kp, vp, global_config, gemma4_kv_cache_layer_index(l, true), scale,
-          ref_split, ref_splits, batch_count, ints + kHeaderError, stream);
+          token_position, kp, lp.q_norm_w != nullptr ? nullptr : vp, global_config,
+          gemma4_kv_cache_layer_index(l, true), scale, ref_split, ref_splits, batch_count,
+          ints + kHeaderError, stream, lp.q_norm_w, lp.k_norm_w, lp.cos[1], lp.sin[1]);
       if (e != hipSuccess) return e;
       qp += rows * kRefDim;
       op += rows * kRefDim;
       kp += (int64_t)batch_count * kRefDim;
       vp += (int64_t)batch_count * kRefDim;
+      if (lp.q_norm_w != nullptr) {
+        lp.q_norm_w += kRefDim;
+        lp.k_norm_w += kRefDim;
+      }
       ++l;
       continue;
     }
     int32_t run = 0;
     while (l + run < last && !is_global(l + run)) ++run;
     const hipError_t e = step_run(op, qp, kp, vp, ck, cv, pt, cfg, seq_lengths, token_position,
-                                  l, run, scale, batch_count, workspace, stream);
+                                  l, run, scale, batch_count, workspace, stream, lp);
     if (e != hipSuccess) return e;
     qp += run * rows * kSDim;
     op += run * rows * kSDim;
     kp += (int64_t)run * batch_count * kRowElems;
     vp += (int64_t)run * batch_count * kRowElems;
+    if (lp.q_norm_w != nullptr) {
+      lp.q_norm_w += (int64_t)run * kSDim;
+      lp.k_norm_w += (int64_t)run * kSDim;
+    }
     l += run;
   }
   return hipSuccess;
+}
+}  // namespace
+}  // namespace gemma4
+
+extern "C" hipError_t gemma4_decode_step_layers_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
+    const int32_t *sliding_page_table, Gemma4KvCacheConfig sliding_config,
+    gemma4_bf16 *global_cache_k, gemma4_bf16 *global_cache_v,
+    const int32_t *global_page_table, Gemma4KvCacheConfig global_config,
+    const int32_t *seq_lengths, const int32_t *token_position, int32_t first_layer,
+    int32_t layer_count, float scale, int32_t batch_count, void *workspace,
+    size_t workspace_bytes, hipStream_t stream) {
+  return step_layers(out, q, k, v, sliding_cache_k, sliding_cache_v, sliding_page_table,
+                     sliding_config, global_cache_k, global_cache_v, global_page_table,
+                     global_config, seq_lengths, token_position, first_layer, layer_count, scale,
+                     batch_count, workspace, workspace_bytes, stream, StepPrep{});
+}
+
+extern "C" hipError_t gemma4_decode_step_layers_prep_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
+    const int32_t *sliding_page_table, Gemma4KvCacheConfig sliding_config,
+    gemma4_bf16 *global_cache_k, gemma4_bf16 *global_cache_v,
+    const int32_t *global_page_table, Gemma4KvCacheConfig global_config,
+    const int32_t *seq_lengths, const int32_t *token_position, const gemma4_bf16 *q_norm_weight,
+    const gemma4_bf16 *k_norm_weight, const float *sliding_cos, const float *sliding_sin,
+    const float *global_cos, const float *global_sin, int32_t first_layer, int32_t layer_count,
+    float scale, int32_t batch_count, void *workspace, size_t workspace_bytes,
+    hipStream_t stream) {
+  bool has_sliding = false, has_global = false;
+  for (int32_t l = first_layer; l >= 0 && l < first_layer + layer_count && l < kNumModelLayers;
+       ++l) {
+    const bool g = l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0;
+    has_global |= g;
+    has_sliding |= !g;
+  }
+  if (q_norm_weight == nullptr || k_norm_weight == nullptr ||
+      (has_sliding && (sliding_cos == nullptr || sliding_sin == nullptr)) ||
+      (has_global && (global_cos == nullptr || global_sin == nullptr)))
+    return hipErrorInvalidValue;
+  StepPrep prep;
+  prep.q_norm_w = reinterpret_cast<const uint16_t *>(q_norm_weight);
+  prep.k_norm_w = reinterpret_cast<const uint16_t *>(k_norm_weight);
+  prep.cos[0] = sliding_cos;
+  prep.sin[0] = sliding_sin;
+  prep.cos[1] = global_cos;
+  prep.sin[1] = global_sin;
+  return step_layers(out, q, k, v, sliding_cache_k, sliding_cache_v, sliding_page_table,
+                     sliding_config, global_cache_k, global_cache_v, global_page_table,
+                     global_config, seq_lengths, token_position, first_layer, layer_count, scale,
+                     batch_count, workspace, workspace_bytes, stream, prep);
 }
 
 extern "C" hipError_t gemma4_decode_walk_bf16(

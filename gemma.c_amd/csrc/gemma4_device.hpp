@@ -79,6 +79,16 @@ __device__ __forceinline__ float xor_lane32(float v) {
   return __builtin_bit_cast(float, __lane_id() < 32 ? swapped[1] : swapped[0]);
 }
 
+// Value of lane (lane ^ 16) with v_permlane16_swap (a VALU exchange of
+// adjacent 16-lane rows, no LDS round trip): with both operands x, result
+// [1] holds the odd rows' values in the even rows and [0] the even rows'
+// values in the odd rows.
+__device__ __forceinline__ float xor_lane16(float v) {
+  const unsigned bits = __builtin_bit_cast(unsigned, v);
+  const auto swapped = __builtin_amdgcn_permlane16_swap(bits, bits, false, false);
+  return __builtin_bit_cast(float, (__lane_id() & 16) == 0 ? swapped[1] : swapped[0]);
+}
+
 // Value of lane (lane ^ kMask): quad DPP for 1 and 2, ds_swizzle within 32
 // lanes, permlane32 swap across the two halves of the wave.
 template <int kMask>

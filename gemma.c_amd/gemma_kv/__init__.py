@@ -114,6 +114,9 @@ SIGNATURES = {
         _I32, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _CFG, _I32, _F32, _I32, _I32, _I32, _P]),
     "gemma4_decode_step_inject_stall": (_I32, [_P, _I32, ctypes.c_uint32, _P]),
     "gemma4_decode_step_set_cooperative": (_I32, [_I32]),
+    "gemma4_decode_step_layers_prep_bf16": (
+        _I32, [_P, _P, _P, _P, _P, _P, _P, _CFG, _P, _P, _P, _CFG, _P, _P, _P, _P, _P, _P, _P, _P,
+               _I32, _I32, _F32, _I32, _P, ctypes.c_size_t, _P]),
     "gemma4_decode_walk_bf16": (
         _I32, [_P] * 7 + [_CFG, _I32, _P, _P, _I32, _F32, _I32, _P, ctypes.c_size_t, _P]),
     "gemma4_runtime_decode_walk": (_I32, [_P, _I32, _P]),
@@ -336,6 +339,21 @@ def decode_step_layers_bf16(out, q, k, v, sliding_k, sliding_v, sliding_page_tab
         ptr(global_page_table), global_config, ptr(seq_lengths), ptr(token_position),
         first_layer, layer_count, softmax_scale, batch_count, ptr(workspace),
         workspace.numel() * workspace.element_size(), stream_handle(stream))
+
+
+def decode_step_layers_prep_bf16(out, q, k, v, sliding_k, sliding_v, sliding_page_table,
+                                 sliding_config, global_k, global_v, global_page_table,
+                                 global_config, seq_lengths, token_position, q_norm_weight,
+                                 k_norm_weight, sliding_cos, sliding_sin, global_cos, global_sin,
+                                 first_layer, layer_count, softmax_scale, batch_count, workspace,
+                                 stream=None) -> int:
+    return lib().gemma4_decode_step_layers_prep_bf16(
+        ptr(out), ptr(q), ptr(k), ptr(v), ptr(sliding_k), ptr(sliding_v),
+        ptr(sliding_page_table), sliding_config, ptr(global_k), ptr(global_v),
+        ptr(global_page_table), global_config, ptr(seq_lengths), ptr(token_position),
+        ptr(q_norm_weight), ptr(k_norm_weight), ptr(sliding_cos), ptr(sliding_sin),
+        ptr(global_cos), ptr(global_sin), first_layer, layer_count, softmax_scale, batch_count,
+        ptr(workspace), workspace.numel() * workspace.element_size(), stream_handle(stream))
 
 
 def decode_walk_bf16(out, q, k, v, cache_k, cache_v, page_table, config, layer,

@@ -306,6 +306,32 @@ hipError_t gemma4_decode_step_layers_bf16(
     int32_t layer_count, float scale, int32_t batch_count, void *workspace,
     size_t workspace_bytes, hipStream_t stream);
 
+// The same step from the layers' raw projections, as the reference's fused
+// decode layer takes them (src/gemma4_flash_attention_decode.cu:216-375,
+// 1036-1067: per-head Q/K RMSNorm with learned weights, split-half RoPE at
+// the token's position, scale-free RMSNorm of V, then append + attention).
+// q, k, v: raw rows in the layout above. q_norm_weight, k_norm_weight: each
+// launch layer's weights back to back ([layer_count][head_dim] at each
+// layer's geometry). RoPE tables [position][rotary_dim / 2] fp32: sliding
+// layers use sliding_cos/sin (rotary over all 256 dims), global layers
+// global_cos/sin (8 x 256: all 256 dims; 1 x 512: the first 128 dims, the
+// runtime state's global tables; there V is derived from the raw K and `v`'s
+// global rows are not read). A prepared value can differ from the reference
+// per-head preparation by one bf16 ulp (the sum of squares is reduced in
+// another order). Otherwise as gemma4_decode_step_layers_bf16;
+// the tables of a kind that the layer range does not use may be null.
+hipError_t gemma4_decode_step_layers_prep_bf16(
+    gemma4_bf16 *out, const gemma4_bf16 *q, const gemma4_bf16 *k, const gemma4_bf16 *v,
+    gemma4_bf16 *sliding_cache_k, gemma4_bf16 *sliding_cache_v,
+    const int32_t *sliding_page_table, Gemma4KvCacheConfig sliding_config,
+    gemma4_bf16 *global_cache_k, gemma4_bf16 *global_cache_v,
+    const int32_t *global_page_table, Gemma4KvCacheConfig global_config,
+    const int32_t *seq_lengths, const int32_t *token_position, const gemma4_bf16 *q_norm_weight,
+    const gemma4_bf16 *k_norm_weight, const float *sliding_cos, const float *sliding_sin,
+    const float *global_cos, const float *global_sin, int32_t first_layer, int32_t layer_count,
+    float scale, int32_t batch_count, void *workspace, size_t workspace_bytes,
+    hipStream_t stream);
+
 // ---- persistent walk over decode steps of one layer ----------------------
 // `steps` consecutive decode steps of one 8 x 256 cache layer in one
 // persistent launch (the same kernel, placement and workspace as the step
