@@ -517,7 +517,12 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
     };
     // A split longer than the row tables hold would drop keys: report it.
+    // Only the kinds of cache this launch reads (a run of sliding layers
+    // never reads the global cache).
+    bool uses[2] = {false, false};
+    for (int32_t l = 0; l < p.layer_count; ++l) uses[is_global_i(l) ? 1 : 0] = true;
     for (int kind = 0; kind < (kWalk ? 1 : 2); ++kind) {
+      if (!uses[kind]) continue;
       const Gemma4KvCacheConfig &c = p.c[kind];
       const int32_t last_len = seq_at(p.layer_count - 1);  // the longest iteration
       int32_t first = c.window_size > 0 ? last_len - c.window_size : 0;
@@ -1370,8 +1375,12 @@ hipError_t step_check(gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
                       int32_t first_layer, int32_t layer_count, int32_t batch_count) {
   const WorkspaceLayout w = workspace_layout(batch_count);
   bool need_kind[2] = {false, false};
-  for (int32_t l = first_layer; l < first_layer + layer_count; ++l)
-    need_kind[(l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0) ? 1 : 0] = true;
+  int32_t last_index[2] = {-1, -1};  // highest cache layer of each kind in use
+  for (int32_t l = first_layer; l < first_layer + layer_count; ++l) {
+    const int kind = (l == kNumModelLayers - 1 || (l + 1) % kGlobalPeriod == 0) ? 1 : 0;
+    need_kind[kind] = true;
+    last_index[kind] = gemma4_kv_cache_layer_index(l, kind == 1);
+  }
   for (int kind = 0; kind < 2; ++kind) {
     if (!need_kind[kind]) continue;
     const Gemma4KvCacheConfig &c = cfg[kind];
@@ -1382,7 +1391,8 @@ hipError_t step_check(gemma4_bf16 *const ck[2], gemma4_bf16 *const cv[2],
     const int64_t live = kind == 0 ? c.window_size : (int64_t)c.max_pages_per_seq * c.page_size;
     if ((live + w.splits - 1) / w.splits > kMaxSplitKeys) return hipErrorInvalidValue;
     const int64_t rows = (int64_t)c.num_layers * c.num_pages * c.page_size;
-    if (rows * kRowElems >= (int64_t)1 << 31 || c.num_layers < 1) return hipErrorInvalidValue;
+    if (rows * kRowElems >= (int64_t)1 << 31 || last_index[kind] >= c.num_layers)
+      return hipErrorInvalidValue;
   }
   return hipSuccess;
 }

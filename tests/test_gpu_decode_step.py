@@ -131,14 +131,14 @@ REF_CASES = [
 ]
 
 
-def _ref_case(rng, first, count, seq, window, s_page, g_page):
+def _ref_case(rng, first, count, seq, window, s_page, g_page, g_layers=8):
     """Inputs and oracle results of a step in the reference model's geometry
     (sliding 8 x 256, global 1 x 512); q/k/v rows flattened layer by layer at
     each layer's width."""
     batch = len(seq)
     layers = list(range(first, first + count))
     n_s = sum(1 for l in range(48) if not is_global(l))
-    n_g = 48 - n_s
+    n_g = g_layers
     s_max = ring_pages(window, s_page)
     g_max = (max(seq) + g_page - 1) // g_page
     s_cfg = cache_config(n_s, batch, s_page, s_max, HEADS, DIM, window)
@@ -213,6 +213,22 @@ def test_decode_step_reference_global_geometry(dev, first, count, seq, window, s
     for i, layer in enumerate(c["layers"]):
         assert np.array_equal(again[i], first_rows[i]), f"layer {layer}"
         assert_close(first_rows[i], c["exp_out"][i], f"layer {layer}")
+
+
+def test_decode_step_reference_geometry_long_global(dev):
+    """A long 1 x 512 global context (17000 keys at batch 2) in the reference
+    geometry: the persistent runs of sliding layers never read the global
+    cache, so its length must not fail their split-length check; the global
+    layer runs as its own fused append + split-K launch with the combine.
+    Same results as the oracle."""
+    c = _ref_case(np.random.default_rng(17), 3, 4, [17000, 5], 128, 1, 64, g_layers=1)
+    d = {n: to_dev(a, dev) for n, a in c["caches"].items()}
+    ws = _workspace(dev, 2)
+    rows = _ref_run(dev, ws, c, d)
+    for n in c["caches"]:
+        assert np.array_equal(from_dev_bf16(d[n]).reshape(c["caches"][n].shape), c["exp"][n]), n
+    for i, layer in enumerate(c["layers"]):
+        assert_close(rows[i], c["exp_out"][i], f"layer {layer}")
 
 
 def test_decode_step_failure_sticky_reference_geometry(dev):
@@ -454,3 +470,29 @@ def test_decode_step_reference_geometry_rejects_before_any_launch(dev):
             assert np.array_equal(from_dev_bf16(d[n]).reshape(c["caches"][n].shape),
                                   c["caches"][n]), n
     assert gk.decode_step_status(ws) == 0
+
+
+def test_decode_step_rejects_cache_layers_out_of_range(dev):
+    """A cache config whose num_layers does not cover a layer of the step
+    (8 x 256 global cache of one layer; layers 0..11 use global cache layers
+    0 and 1) is rejected before the launch: no output written, caches as
+    they were."""
+    import torch
+    rng = np.random.default_rng(5)
+    layers, s_cfg, g_cfg, s_pt, g_pt, caches, q, k, v = _case(rng, 0, 12, [40], 64, 1, 16)
+    short = list(g_cfg)
+    short[0] = 1
+    dcaches = {n: to_dev(a, dev) for n, a in caches.items()}
+    ws = _workspace(dev, 1)
+    out = empty_bf16((12, 1, 16, DIM), dev)
+    out.fill_(0x1234)
+    code = gk.decode_step_layers_bf16(
+        out, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), dcaches["sk"], dcaches["sv"],
+        to_dev(s_pt, dev), gk.make_config(*s_cfg), dcaches["gk"], dcaches["gv"],
+        to_dev(g_pt, dev), gk.make_config(*short), to_dev(np.asarray([40], np.int32), dev),
+        to_dev(np.asarray([39], np.int32), dev), 0, 12, 0.0625, 1, ws)
+    assert code == gk.HIP_ERROR_INVALID_VALUE
+    torch.cuda.synchronize()
+    assert (out == 0x1234).all()
+    for n in caches:
+        assert np.array_equal(from_dev_bf16(dcaches[n]).reshape(caches[n].shape), caches[n]), n
