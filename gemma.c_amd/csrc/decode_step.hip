@@ -181,11 +181,23 @@ __device__ __forceinline__ int32_t cache_layer_of(int32_t layer) {
   return index;
 }
 
-// Workgroup barrier of the step kernel. A barrier that waits only for LDS
-// traffic (leaving register-tile loads and LDS DMA in flight across it) was
-// measured no faster (392 against 382 us per config-2 step): the first use
-// of a register tile waits for it anyway.
-__device__ __forceinline__ void step_barrier() { __syncthreads(); }
+// Workgroup barrier of the step kernel. The step's barriers order LDS traffic only: each wave's LDS operations
+// complete, then s_barrier (inline asm, so the compiler adds no wait for
+// vector memory operations). Tile loads and LDS DMA stay in flight across
+// it; global-memory ordering the step needs is explicit (the prefetch
+// wave's DMA wait before a global layer, the control wave's store wait
+// before its flag, a walk's append wait). With __syncthreads every wave
+// first waited for all of its outstanding loads: 383.4-383.8 against
+// 376.5 us per config-2 step. Walks keep __syncthreads (4.44 against 4.54
+// us per step).
+template <bool kLdsOnly>
+__device__ __forceinline__ void step_barrier() {
+  if constexpr (kLdsOnly) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  } else {
+    __syncthreads();
+  }
+}
 
 __device__ __forceinline__ uint64_t now_ticks() { return __builtin_amdgcn_s_memrealtime(); }
 
@@ -365,7 +377,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
     s_stall_layer = (int32_t)h0[kHeaderStallLayer] - 1;
     s_stall_ticks = (int32_t)h1[kHeaderStallTicks - 4];
   }
-  step_barrier();
+  step_barrier<!kWalk>();
   const int32_t ticket = wave_uniform(s_ticket);
   const bool active = ticket < p.batch * p.splits;
   const int32_t b = active ? ticket % p.batch : 0;
@@ -488,11 +500,11 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         request(kLdsSlots);
         wait_stores_complete();
       }
-      step_barrier();  // A
+      step_barrier<!kWalk>();  // A
       if (target > i) request(kSlotsPerInterval);
-      step_barrier();  // B
+      step_barrier<!kWalk>();  // B
       if (target > i) request(kSlotsPerInterval);
-      step_barrier();  // C
+      step_barrier<!kWalk>();  // C
       maybe_plan(i);
       if (target > i) request(kSlotsPerInterval);
     }
@@ -647,8 +659,8 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         s_new[lane] = np;
       }
       STEP_MARK(2);
-      step_barrier();  // A: layer i may start
-      step_barrier();  // B: this workgroup's compute waves finished layer i
+      step_barrier<!kWalk>();  // A: layer i may start
+      step_barrier<!kWalk>();  // B: this workgroup's compute waves finished layer i
       STEP_MARK(5);
 
       // Combine unit u's splits for the 8-dim chunks c = split, split +
@@ -732,7 +744,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
         }
       }
       STEP_MARK(6);
-      step_barrier();  // C: records read; compute waves may prefetch
+      step_barrier<!kWalk>();  // C: records read; compute waves may prefetch
       // My output slices and chunk resets are complete before my local flag.
       wait_stores_complete();
       if (lane == 0) {
@@ -1022,7 +1034,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
   const int32_t rec_ml = (rec_d / kPackElems * kChunkFloats + rec_g * kHalfChunk + kPackElems) * 4;
 
   for (int32_t i = 0; i < p.layer_count; ++i) {
-    step_barrier();  // A: layer i-1 published (or i == 0), inputs in LDS
+    step_barrier<!kWalk>();  // A: layer i-1 published (or i == 0), inputs in LDS
     STEP_MARK(3);
     const LayerView view = cur;
     // A walk appends first, so the store has landed long before barrier B.
@@ -1121,7 +1133,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       }
     }
     STEP_MARK(4);
-    step_barrier();  // B
+    step_barrier<!kWalk>();  // B
     if (kFloor < 2 && active) {
       float big_m = -INFINITY;
 #pragma unroll
@@ -1152,7 +1164,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
       if (rec_d % kPackElems == 0) local_store2(rec_buf, rec + rec_ml, big_m, big_l);
     }
     STEP_MARK(9);
-    step_barrier();  // C: the control wave has read the split records
+    step_barrier<!kWalk>();  // C: the control wave has read the split records
     prepare(i);
   }
 }
