@@ -42,6 +42,29 @@
 constexpr size_t kNoAllocScratchBytes = size_t(40) << 20;
 static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
+// Development builds only (-DSPLIT_TRACE=1): real-time stamps of the split
+// kernel's phases, [workgroup][wave][8], read with gemma4_debug_split_trace.
+#ifndef SPLIT_TRACE
+#define SPLIT_TRACE 0
+#endif
+#if SPLIT_TRACE
+__device__ uint64_t g_split_trace[8192 * 4 * 8];
+#define SPLIT_MARK(k)                                                                        \
+  do {                                                                                       \
+    if (__lane_id() == 0)                                                                    \
+      g_split_trace[(((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * \
+                        32 +                                                                 \
+                    (threadIdx.x / 64) * 8 + (k)] = __builtin_amdgcn_s_memrealtime();        \
+  } while (0)
+extern "C" hipError_t gemma4_debug_split_trace(void *dst, size_t bytes) {
+  return hipMemcpyFromSymbol(dst, HIP_SYMBOL(g_split_trace), bytes, 0, hipMemcpyDeviceToHost);
+}
+#else
+#define SPLIT_MARK(k) \
+  do {                \
+  } while (0)
+#endif
+
 namespace gemma4 {
 namespace {
 
@@ -224,6 +247,16 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   const int32_t b = blockIdx.z;
   const Gemma4KvCacheConfig &c = p.c;
 
+  SPLIT_MARK(0);
+  // A global cache's split begins at split * split_size whatever the length,
+  // so the page-table entry of this lane's first key is requested before the
+  // length arrives (one dependent round trip fewer before the first tile).
+  const bool early_page = !Sh::kStaged && c.window_size == 0;
+  int32_t first_page = 0;
+  if (early_page) {
+    const int32_t key0 = split * p.split_size + key_lane * Sh::CT * Sh::KT + lane;
+    first_page = p.page_table[b * c.max_pages_per_seq + (key0 / c.page_size) % c.max_pages_per_seq];
+  }
   const int32_t seq_len = wave_uniform(p.seq_lengths[b]);
   int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;
   first = first < 0 ? 0 : first;
@@ -305,6 +338,7 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   const int32_t begin = first + split * p.split_size;
   const int32_t end = min(seq_len, begin + p.split_size);
 
+  SPLIT_MARK(1);
   // ---- Q for the GW heads of this wave, 8 dims per lane, pre-scaled
   // Q stays packed bf16 (two dims per register): Q·K runs on v_dot2 with
   // exact products and fp32 sums; the softmax scale is applied to the sum.
@@ -590,7 +624,8 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   // flight for a whole chunk. Every load is issued on every path, so the
   // memory wait counters stay exact.
   static_assert(CT % 2 == 0, "tiles per chunk alternate between two buffers");
-    publish(0, page_row(0, fetch_page(0)));
+    publish(0, page_row(0, early_page ? first_page : fetch_page(0)));
+    SPLIT_MARK(2);
     int32_t next_page = fetch_page(1);
     TileBuf buf0, buf1;
     issue(buf0, 0, 0);
@@ -599,6 +634,7 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
       for (int t = 0; t < CT; t += 2) {
         issue(buf1, m, t + 1);
         if (m * CT + t < my_tiles) compute(buf0);
+        if (m == 0 && t == 0) SPLIT_MARK(3);
         if (t + 2 < CT) {
           issue(buf0, m, t + 2);
         } else {
@@ -611,6 +647,7 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
     }
   }
 
+  SPLIT_MARK(4);
   // ---- wave totals: l per head, acc summed over the RPL key rows
   float l_head[GW];
   gather_heads<GW, S>(reduce_sum_from<(1 << S) * GW>(l_lane), my_g, l_head);
@@ -671,6 +708,7 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
     }
   }
 
+  SPLIT_MARK(5);
   // ---- emit: the bf16 row when this split is the whole row, else partials
   const bool emitter = key_lane == 0 && r == 0;
   // With in-kernel combining, a row with one live split needs no partials.
@@ -711,6 +749,7 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
       }
     }
   }
+  SPLIT_MARK(6);
   if (whole_row || p.counters == nullptr) return;
 
   // ---- in-kernel combine: the last split workgroup of (b, head) to finish
