@@ -89,8 +89,11 @@ __device__ __forceinline__ float xor_lane16(float v) {
   return __builtin_bit_cast(float, (__lane_id() & 16) == 0 ? swapped[1] : swapped[0]);
 }
 
-// Value of lane (lane ^ kMask): quad DPP for 1 and 2, ds_swizzle within 32
-// lanes, permlane32 swap across the two halves of the wave.
+// Value of lane (lane ^ kMask): quad DPP for 1 and 2, DPP row_ror:8 for 8
+// (rotating a 16-lane row by 8 is exactly xor 8), v_permlane16_swap for 16,
+// permlane32 swap across the two halves of the wave; other masks by
+// ds_swizzle within 32 lanes. The DPP and permlane forms are VALU exchanges
+// without an LDS round trip.
 template <int kMask>
 __device__ __forceinline__ float lane_xor(float v) {
   static_assert(kMask > 0 && kMask < kWave, "lane mask");
@@ -98,6 +101,10 @@ __device__ __forceinline__ float lane_xor(float v) {
     return dpp_move<0xB1>(v);  // quad_perm [1,0,3,2]
   } else if constexpr (kMask == 2) {
     return dpp_move<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (kMask == 8) {
+    return dpp_move<0x128>(v);  // row_ror:8
+  } else if constexpr (kMask == 16) {
+    return xor_lane16(v);
   } else if constexpr (kMask < 32) {
     return swizzle_xor<kMask>(v);
   } else if constexpr (kMask == 32) {
