@@ -89,11 +89,12 @@ __device__ __forceinline__ float xor_lane16(float v) {
   return __builtin_bit_cast(float, (__lane_id() & 16) == 0 ? swapped[1] : swapped[0]);
 }
 
-// Value of lane (lane ^ kMask): quad DPP for 1 and 2, DPP row_ror:8 for 8
-// (rotating a 16-lane row by 8 is exactly xor 8), v_permlane16_swap for 16,
-// permlane32 swap across the two halves of the wave; other masks by
-// ds_swizzle within 32 lanes. The DPP and permlane forms are VALU exchanges
-// without an LDS round trip.
+// Value of lane (lane ^ kMask): quad DPP for 1 and 2, two row rotates and a
+// select for 4, DPP row_ror:8 for 8 (rotating a 16-lane row by 8 is exactly
+// xor 8), v_permlane16_swap for 16, permlane32 swap across the two halves of
+// the wave; a mask of several bits is one exchange per group of bits. All
+// are VALU exchanges without an LDS round trip (ds_swizzle remains only for
+// masks spanning bits 3 and 4 together).
 template <int kMask>
 __device__ __forceinline__ float lane_xor(float v) {
   static_assert(kMask > 0 && kMask < kWave, "lane mask");
@@ -101,16 +102,26 @@ __device__ __forceinline__ float lane_xor(float v) {
     return dpp_move<0xB1>(v);  // quad_perm [1,0,3,2]
   } else if constexpr (kMask == 2) {
     return dpp_move<0x4E>(v);  // quad_perm [2,3,0,1]
+  } else if constexpr (kMask == 4) {
+    // Within a 16-lane row: lanes with bit 2 set read lane - 4 (row_ror:4),
+    // the others lane + 4 (row_ror:12).
+    const float down = dpp_move<0x124>(v), up = dpp_move<0x12C>(v);
+    return (__lane_id() & 4) ? down : up;
   } else if constexpr (kMask == 8) {
     return dpp_move<0x128>(v);  // row_ror:8
   } else if constexpr (kMask == 16) {
     return xor_lane16(v);
+  } else if constexpr (kMask < 32 && (kMask & 7) != 0 && (kMask & ~7) != 0) {
+    // Masks over both the quad/row bits and bits 3..4: one exchange each.
+    return lane_xor<kMask & ~7>(lane_xor<kMask & 7>(v));
+  } else if constexpr (kMask < 32 && (kMask & 3) != 0 && (kMask & 4) != 0) {
+    return lane_xor<4>(lane_xor<kMask & 3>(v));
   } else if constexpr (kMask < 32) {
     return swizzle_xor<kMask>(v);
   } else if constexpr (kMask == 32) {
     return xor_lane32(v);
   } else {
-    return xor_lane32(swizzle_xor<kMask - 32>(v));
+    return xor_lane32(lane_xor<kMask - 32>(v));
   }
 }
 
