@@ -301,6 +301,11 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
         s2[pos & 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8_t, kf[s]), __builtin_bit_cast(bf16x8_t, qreg[s]),
             s2[pos & 1], 0, 0, 0);
+        // Keep each fragment's wait right before its MFMA: without this
+        // fence the scheduler issued all sixteen waits first, one
+        // lgkmcnt(0) in effect, and the reads no longer overlapped the
+        // MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
       });
       return s2[0] + s2[1];
     };
