@@ -487,6 +487,9 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
             copy_row_pair(vsrc[pos / 2], v_dst[S ^ 1] + (pos / 2) * 2 * kRowBytes);
           }
         }
+        // Each fragment's wait stays right before its MFMA (the scheduler
+        // otherwise clusters the waits and the reads stop overlapping).
+        __builtin_amdgcn_sched_barrier(0);
       }
     };
     static_for<0, KS>(step_s);
