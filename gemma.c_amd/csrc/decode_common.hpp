@@ -36,6 +36,9 @@ struct DecodeParams {
   // Non-null (persistent decode step only): a nonzero word here turns the
   // launch into zeros for its output rows, with no append.
   const int32_t *gate;
+  // Nonzero: a full ring may be split by ring slot rather than by position
+  // (the partials are internal to the launch).
+  int32_t slot_splits = 0;
 };
 
 constexpr int kRowInvalid = -1;   // key outside the split or unmapped page
