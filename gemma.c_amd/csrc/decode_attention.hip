@@ -676,6 +676,24 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
       }
       __syncthreads();  // the table and the stages are free for the next window
     }
+  } else if (my_tiles > 0 && my_tiles <= 2) {
+    // A wave with one or two tiles (the sliding layers' short splits) runs
+    // them straight: the pipeline below would also issue the loads of the
+    // dead tiles up to the end of the chunk and wait for them before exit.
+    publish(0, page_row(0, early_ok ? early_page : fetch_page(0)));
+    SPLIT_MARK(2);
+    TileBuf buf0, buf1;
+    issue(buf0, 0, 0);
+    load_q();
+    if (my_tiles == 2) {
+      issue(buf1, 0, 1);
+      compute(buf0);
+      SPLIT_MARK(3);
+      compute(buf1);
+    } else {
+      compute(buf0);
+      SPLIT_MARK(3);
+    }
   } else if (my_tiles > 0) {
   // Software pipeline over my chunks, CT tiles each, fully unrolled inside a
   // chunk so both register buffers are static: tile t+1's loads are in flight
@@ -1268,11 +1286,13 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
       max_live_keys < 0 || config.num_heads <= 0) {
     return hipErrorInvalidValue;
   }
-  int32_t tile;
+  int32_t tile, key_tile;
   if (config.num_heads == 8 && config.head_dim == 256) {
     tile = SlidingShape::KT * SlidingShape::CT;  // one wave's page-lookup chunk
+    key_tile = SlidingShape::KT;
   } else if (config.num_heads == 1 && config.head_dim == 512) {
     tile = GlobalRefShape::KT * GlobalRefShape::CT;
+    key_tile = GlobalRefShape::KT;
   } else {
     return hipErrorInvalidValue;
   }
@@ -1282,7 +1302,8 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
   // tail). A batch is sized by its longest sequence, so shorter ones leave
   // workgroups idle: 32 per CU then (measured best on 64 sequences of 512 to
   // 32768 keys).
-  if (target_workgroups <= 0) target_workgroups = batch_count > 1 ? 8192 : 256;
+  const bool planned = target_workgroups <= 0;
+  if (planned) target_workgroups = batch_count > 1 ? 8192 : 256;
   const int64_t keys = (int64_t)std::max(max_live_keys, 1);
   const int64_t heads = (int64_t)batch_count * config.num_heads;
   int64_t splits_per_seq = (target_workgroups + heads - 1) / heads;
@@ -1290,6 +1311,15 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
   int64_t size = (keys + splits_per_seq - 1) / splits_per_seq;
   size = ((size + tile - 1) / tile) * tile;
   if (size < tile) size = tile;
+  // One sequence whose splits come out at two tiles or fewer (a sliding
+  // layer's 1024-key window): the split is a dependent chain of tile
+  // latencies, so one tile per workgroup, as long as that stays within two
+  // workgroups per CU (1024 keys: 8.5 against 9.4 us per layer with the
+  // combine, 512 against 256 workgroups).
+  if (planned && batch_count == 1 && size <= 2 * key_tile &&
+      heads * ((keys + key_tile - 1) / key_tile) <= 2 * target_workgroups) {
+    size = key_tile;
+  }
   *split_size = (int32_t)size;
   *num_splits = (int32_t)((keys + size - 1) / size);
   return hipSuccess;

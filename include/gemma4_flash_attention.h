@@ -207,7 +207,9 @@ hipError_t gemma4_flash_attention_global_fwd_bf16_norm_rope(
 // Split plan for the MI355X: the split size (a multiple of the kernel's key
 // wave chunk) that gives about `target_workgroups` split workgroups (0 = default:
 // one per CU for one sequence, 32 per CU for a batch) for `batch_count` sequences of up to `max_live_keys` live keys,
-// and the split count that covers `max_live_keys`. Replaces the fixed
+// and the split count that covers `max_live_keys`. With the default target,
+// one sequence whose splits would hold two key tiles or fewer (a 1024-key
+// sliding window) gets one-tile splits instead, up to two workgroups per CU. Replaces the fixed
 // GEMMA4_SLIDING_DECODE_SPLIT_SIZE (src/gemma4.h:24) and the active split
 // count of src/gemma4_decode_megakernel.cu:158-167.
 hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,

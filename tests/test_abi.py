@@ -87,7 +87,13 @@ def test_ensure_page_ring_matches_oracle():
 def test_split_plan_fills_the_chip():
     c = gk.make_config(40, 1024, 1, 1024, 1, 8, 256, 1024)
     size, n = gk.decode_split_plan(c, 1, 1024)
-    assert size % 32 == 0 and size * n >= 1024 and 8 * n >= 256
+    assert size * n >= 1024 and 8 * n >= 256
+    # A 1024-key window at one sequence: one 16-key tile per workgroup (512
+    # workgroups, two per CU).
+    assert (size, n) == (16, 64)
+    # An explicit target keeps whole 32-key chunks.
+    size, n = gk.decode_split_plan(c, 1, 1024, 256)
+    assert (size, n) == (32, 32)
     c = gk.make_config(8, 128, 64, 128, 1, 8, 256, 0)
     size, n = gk.decode_split_plan(c, 1, 8192)
     assert size * n >= 8192 and 8 * n >= 256
