@@ -194,8 +194,8 @@ __device__ __forceinline__ uint4 prep_pack(uint4 raw, const uint16_t *weight,
   ss += lane_xor<2>(ss);
   ss += lane_xor<4>(ss);
   ss += lane_xor<8>(ss);
-  ss += lane_xor<16>(ss);
-  if constexpr (LPR == 64) ss += lane_xor<32>(ss);
+  ss = xor_sum<16>(ss);
+  if constexpr (LPR == 64) ss = xor_sum<32>(ss);
   const float scale = 1.0f / sqrtf(ss / (float)(LPR * kPackElems) + kRmsEps);
   float y[8];
   if (weight == nullptr) {
@@ -231,7 +231,19 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   __shared__ int32_t s_rows[Sh::kMaxW][2][kWave];
   __shared__ float s_prob[Sh::kMaxW][kWave];
   __shared__ float s_ml[Sh::kMaxW][2][GW];
-  __shared__ __attribute__((aligned(16))) float s_acc[Sh::kMaxW][GW][D];
+  // Staged shapes: kStages stages of K and V rows for kStepKeys keys (one
+  // KT-key tile per key lane per step), rows of kWindowKeys keys at a time.
+  constexpr int kStages = 2;
+  constexpr int kLanes = Sh::kMaxW / HG;  // key lanes: tiles per step
+  constexpr int kStepKeys = kLanes * KT;
+  constexpr int kWindowKeys = Sh::kMaxW * kWave;
+  constexpr int kStageUint4 = Sh::kStaged ? kStages * 2 * kStepKeys * LPR : 0;
+  constexpr int kAccUint4 = Sh::kMaxW * GW * D / 4;
+  // The cross-wave merge buffer s_acc shares LDS with the stages: the merge
+  // runs after the last step's barrier.
+  __shared__ __attribute__((aligned(1024)))
+  uint4 s_lds[kStageUint4 > kAccUint4 ? kStageUint4 : kAccUint4];
+  auto s_acc = reinterpret_cast<float (*)[GW][D]>(&s_lds[0]);
 
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = wave_uniform(threadIdx.x / kWave);  // scalar: wave-uniform control flow
@@ -557,9 +569,12 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
       // permute per word pair (28.8 against 31.6 us at 8193 keys). The 8x256
       // shape keeps the fp32 FMA form: the dot2 form measured 1.7% slower on
       // the HBM-bound batch-64 leg.
+      // Staged tiles hold zero rows for unreadable keys (their probability
+      // is 0 as well), so only register-loaded tiles mask V.
 #pragma unroll
       for (int kl = 0; kl < LOADS; kl += 2) {
-        const bool ok0 = (t.valid >> kl) & 1u, ok1 = (t.valid >> (kl + 1)) & 1u;
+        const bool ok0 = Sh::kStaged || ((t.valid >> kl) & 1u);
+        const bool ok1 = Sh::kStaged || ((t.valid >> (kl + 1)) & 1u);
         const uint32_t a[4] = {ok0 ? t.v[kl].x : 0u, ok0 ? t.v[kl].y : 0u, ok0 ? t.v[kl].z : 0u,
                                ok0 ? t.v[kl].w : 0u};
         const uint32_t c[4] = {ok1 ? t.v[kl + 1].x : 0u, ok1 ? t.v[kl + 1].y : 0u,
@@ -600,25 +615,23 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
 
   if constexpr (Sh::kStaged) {
     // Every head group (the 1 x 512 geometry: four groups of four heads)
-    // attends to every key of the split, so each 16-key step (two 8-key
-    // tiles, one per key lane) is copied into LDS once per workgroup -- wave
-    // w copies the K and V rows of keys 2w, 2w + 1 with global_load_lds, or
-    // zeros for an unreadable key -- and the waves read it from there: two
-    // waves per SIMD, one tile each. Two stages, one barrier per step: at
+    // attends to every key of the split, so each step of kStepKeys keys (one
+    // KT-key tile per key lane) is copied into LDS once per workgroup -- wave
+    // w copies the K and V rows of kRowsPerWave keys with global_load_lds,
+    // or zeros for an unreadable key -- and the waves read it from there:
+    // two waves per SIMD, one tile each. Two stages, one barrier per step: at
     // step i a wave waits for its own copies of step i, the barrier
     // publishes them and frees the stage of step i - 1, which then receives
     // step i + 1. Rows of the split's keys come from a table filled once per
     // window of kWindowKeys keys (one page-table load per thread).
-    constexpr int kStages = 2;
-    constexpr int kLanes = Sh::kMaxW / HG;          // key lanes: tiles per step
-    constexpr int kStepKeys = kLanes * KT;
-    constexpr int kWindowKeys = Sh::kMaxW * kWave;
-    static_assert(RPL == 1 && KT == LOADS && kStepKeys == 2 * Sh::kMaxW,
-                  "one row per load; two rows per wave per step");
+    constexpr int kRowsPerWave = kStepKeys / Sh::kMaxW;
+    static_assert(RPL == 1 && KT == LOADS && kStepKeys % Sh::kMaxW == 0 &&
+                      kWindowKeys % kStepKeys == 0,
+                  "one row per load; whole rows per wave per step");
     load_q();
-    __shared__ __attribute__((aligned(1024))) uint4 s_kv[kStages][2][kStepKeys * LPR];
+    auto s_kv = reinterpret_cast<uint4 (*)[2][kStepKeys * LPR]>(&s_lds[0]);
     __shared__ int32_t s_keyrow[kWindowKeys];
-    const uint32_t kv_lds = wave_uniform(lds_address(&s_kv[0][0][0]));
+    const uint32_t kv_lds = wave_uniform(lds_address(&s_lds[0]));
     constexpr uint32_t kRowBytesKV = D * 2;
     constexpr uint32_t kHalfBytes = kStepKeys * kRowBytesKV;  // K (or V) of one stage
     const uint64_t kcache = reinterpret_cast<uint64_t>(p.cache_k + (int64_t)head * D);
@@ -628,8 +641,8 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
     const uint32_t lane_off = (uint32_t)lane * 16;
     auto copy_step = [&](int32_t step, int stage) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int kk = 2 * wave + i;
+      for (int i = 0; i < kRowsPerWave; ++i) {
+        const int kk = kRowsPerWave * wave + i;
         const int32_t row = wave_uniform(s_keyrow[step * kStepKeys + kk]);
         const uint32_t dst = stage * 2 * kHalfBytes + kk * kRowBytesKV;
         if (row == kRowInvalid) {

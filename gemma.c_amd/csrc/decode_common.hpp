@@ -52,7 +52,16 @@ constexpr int kRowNewToken = -2;  // key being appended in this launch
 // value then repeats across those low lanes).
 template <int N, int O>
 __device__ __forceinline__ void split_butterfly(float *v, int lane) {
-  if constexpr (N > 1) {
+  if constexpr (N > 1 && (O == 32 || O == 16)) {
+    // One VALU swap per pair leaves each lane exactly its two addends.
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) {
+      float x, y;
+      swap_halves<O>(v[i], v[i + N / 2], x, y);
+      v[i] = x + y;
+    }
+    split_butterfly<N / 2, O / 2>(v, lane);
+  } else if constexpr (N > 1) {
     const bool hi = (lane & O) != 0;
 #pragma unroll
     for (int i = 0; i < N / 2; ++i) {
@@ -61,6 +70,9 @@ __device__ __forceinline__ void split_butterfly(float *v, int lane) {
       v[i] = keep + lane_pair<O>(send);
     }
     split_butterfly<N / 2, O / 2>(v, lane);
+  } else if constexpr (O == 32 || O == 16) {
+    v[0] = xor_sum<O>(v[0]);
+    split_butterfly<1, O / 2>(v, lane);
   } else if constexpr (O >= 1) {
     v[0] += lane_pair<O>(v[0]);
     split_butterfly<1, O / 2>(v, lane);
@@ -72,7 +84,7 @@ __device__ __forceinline__ void split_butterfly(float *v, int lane) {
 template <int kFrom>
 __device__ __forceinline__ float reduce_max_from(float v) {
   if constexpr (kFrom < kWave) {
-    v = fmaxf(v, lane_xor<kFrom>(v));
+    v = xor_max<kFrom>(v);
     return reduce_max_from<kFrom * 2>(v);
   } else {
     return v;
@@ -81,7 +93,7 @@ __device__ __forceinline__ float reduce_max_from(float v) {
 template <int kFrom>
 __device__ __forceinline__ float reduce_sum_from(float v) {
   if constexpr (kFrom < kWave) {
-    v += lane_xor<kFrom>(v);
+    v = xor_sum<kFrom>(v);
     return reduce_sum_from<kFrom * 2>(v);
   } else {
     return v;
@@ -116,7 +128,7 @@ __device__ __forceinline__ void gather_heads(float mine, int my_g, float (&out)[
 template <int LPR>
 __device__ __forceinline__ float sum_rows(float v) {
   if constexpr (LPR < kWave) {
-    v += lane_xor<LPR>(v);
+    v = xor_sum<LPR>(v);
     return sum_rows<LPR * 2>(v);
   } else {
     return v;

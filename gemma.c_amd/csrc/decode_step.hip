@@ -297,7 +297,7 @@ __device__ __forceinline__ uint4 prep_row(uint4 raw, uint4 weight, bool weighted
   ss += lane_pair<2>(ss);
   ss += lane_pair<4>(ss);
   ss += lane_pair<8>(ss);
-  ss += xor_lane16(ss);
+  ss = xor_sum<16>(ss);
   const float scale = 1.0f / sqrtf(ss / (float)kSDim + kRmsEps);
   float w[8];
   unpack8(weight, w);

@@ -125,6 +125,51 @@ __device__ __forceinline__ float lane_xor(float v) {
   }
 }
 
+// v_permlane32_swap / v_permlane16_swap of (a, b): lanes whose bit 5 (bit 4)
+// is clear receive b from their partner lane ^ 32 (^ 16) in place of their
+// own b, the others receive a from the partner in place of their own a. So
+// result[0] + result[1] is, in a lane with the bit clear, a + a of the
+// partner, and with the bit set, b of the partner + b: one swap serves a
+// value-splitting butterfly step or, with a == b, a symmetric exchange.
+template <int kMask>
+__device__ __forceinline__ void swap_halves(float a, float b, float &x, float &y) {
+  static_assert(kMask == 16 || kMask == 32, "VALU swaps exchange 16- or 32-lane halves");
+  const unsigned ua = __builtin_bit_cast(unsigned, a), ub = __builtin_bit_cast(unsigned, b);
+  const auto s = kMask == 32 ? __builtin_amdgcn_permlane32_swap(ua, ub, false, false)
+                             : __builtin_amdgcn_permlane16_swap(ua, ub, false, false);
+  unsigned sx = s[0], sy = s[1];
+  // hipcc (ROCm 7.2) reads both results from the first result's register
+  // when both feed further arithmetic (v_add v1, v1, v1 after the swap); an
+  // empty asm on the pair keeps the second result's register.
+  asm("" : "+v"(sx), "+v"(sy));
+  x = __builtin_bit_cast(float, sx);
+  y = __builtin_bit_cast(float, sy);
+}
+
+// v + (v of lane ^ kMask) and max(v, v of lane ^ kMask): for masks 16 and 32
+// one swap and one add / max (the select of lane_xor is not needed for a
+// symmetric operation; the result is bit-identical).
+template <int kMask>
+__device__ __forceinline__ float xor_sum(float v) {
+  if constexpr (kMask == 16 || kMask == 32) {
+    float x, y;
+    swap_halves<kMask>(v, v, x, y);
+    return x + y;
+  } else {
+    return v + lane_xor<kMask>(v);
+  }
+}
+template <int kMask>
+__device__ __forceinline__ float xor_max(float v) {
+  if constexpr (kMask == 16 || kMask == 32) {
+    float x, y;
+    swap_halves<kMask>(v, v, x, y);
+    return fmaxf(x, y);
+  } else {
+    return fmaxf(v, lane_xor<kMask>(v));
+  }
+}
+
 // Value of a partner lane that differs from this lane in bit kBit and agrees
 // on every higher bit (lower bits may differ); the pairing is an involution.
 // Butterfly sums only need such a pairing, and row mirrors are plain DPP:

@@ -526,7 +526,7 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
 #pragma unroll
     for (int i = 3; i < 15; i += 2) tmax = fmaxf(fmaxf(tmax, sc[i]), sc[i + 1]);
     tmax = fmaxf(tmax, sc[15]);
-    tmax = fmaxf(tmax, lane_xor<32>(tmax)) * p.q_scale;
+    tmax = xor_max<32>(tmax) * p.q_scale;
     // Lazy maximum: move it (and rescale) only when a row outgrew it by more
     // than the slack; otherwise exp2 arguments stay below the slack.
     if (__builtin_amdgcn_ballot_w64(tmax > m_run + kRescaleSlack) != 0) {
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
 
   if (emit) {
     // Normalise and store: lane holds dims 32d + (i/4)*8 + 4*half + i%4 of row n.
-    l_run += lane_xor<32>(l_run);
+    l_run = xor_sum<32>(l_run);
     if (row_ok) {
       const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
       uint16_t *orow = p.out + (((int64_t)b * Lq + row) * kQueryHeads + qh) * kDim;

@@ -325,8 +325,8 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
       sc[j] = kp <= row ? x : -INFINITY;
       tmax = fmaxf(tmax, sc[j]);
     }
-    tmax = fmaxf(tmax, lane_xor<16>(tmax));
-    tmax = fmaxf(tmax, lane_xor<32>(tmax)) * p.q_scale;
+    tmax = xor_max<16>(tmax);
+    tmax = xor_max<32>(tmax) * p.q_scale;
     if (__builtin_amdgcn_ballot_w64(tmax > m_run + kD512Slack) != 0) {
       const float m_new = fmaxf(m_run, tmax);
       const float alpha = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -382,8 +382,8 @@ __global__ __launch_bounds__(kD512Threads, 1) void prefill_d512_kernel(D512Param
   wait_copies();  // no copy may still be writing LDS when the workgroup exits
 
   // Normalise and store: lane holds head `head`, dims 16 d + 4 g + i.
-  l_run += lane_xor<16>(l_run);
-  l_run += lane_xor<32>(l_run);
+  l_run = xor_sum<16>(l_run);
+  l_run = xor_sum<32>(l_run);
   if (!row_ok) return;
   const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
   uint16_t *orow = p.out + (((int64_t)b * L + row) * kQueryHeads + head) * kD512;
