@@ -1304,7 +1304,10 @@ hipError_t gemma4_decode_split_plan(Gemma4KvCacheConfig config,
     tile = SlidingShape::KT * SlidingShape::CT;  // one wave's page-lookup chunk
     key_tile = SlidingShape::KT;
   } else if (config.num_heads == 1 && config.head_dim == 512) {
-    tile = GlobalRefShape::KT * GlobalRefShape::CT;
+    // The staged kernel's granule is one LDS step (a tile per key lane):
+    // 8193 keys as 171 splits of 48 run split + combine in 20.5 against
+    // 21.8 us as 129 splits of 64 (32 / 80 / 96 keys: 23.7 / 23.2 / 25.2).
+    tile = (GlobalRefShape::kMaxW / GlobalRefShape::HG) * GlobalRefShape::KT;
     key_tile = GlobalRefShape::KT;
   } else {
     return hipErrorInvalidValue;

@@ -700,7 +700,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
           const float l_s = live ? __uint_as_float(got.ml[1]) : 0.0f;
           // Reduce over the splits (lane bits 0..4) of each row g = lane bit 5.
           float big_m = m_s;
-          big_m = fmaxf(big_m, lane_pair<16>(big_m));
+          big_m = xor_max<16>(big_m);
           big_m = fmaxf(big_m, lane_pair<8>(big_m));
           big_m = fmaxf(big_m, lane_pair<4>(big_m));
           big_m = fmaxf(big_m, lane_pair<2>(big_m));
@@ -708,7 +708,7 @@ __global__ __launch_bounds__(kStepThreads) void decode_step_kernel(StepParams p)
           const float m_ref = big_m == -INFINITY ? 0.0f : big_m;
           const float w = l_s > 0.0f ? __builtin_amdgcn_exp2f(m_s - m_ref) : 0.0f;
           float big_l = w * l_s;
-          big_l += lane_pair<16>(big_l);
+          big_l = xor_sum<16>(big_l);
           big_l += lane_pair<8>(big_l);
           big_l += lane_pair<4>(big_l);
           big_l += lane_pair<2>(big_l);

@@ -99,3 +99,6 @@ def test_split_plan_fills_the_chip():
     assert size * n >= 8192 and 8 * n >= 256
     size, n = gk.decode_split_plan(c, 64, 32768)
     assert size * n >= 32768
+    # 1 x 512 (staged 16-key steps): 8193 keys as 171 splits of 48.
+    c = gk.make_config(8, 129, 64, 129, 1, 1, 512, 0)
+    assert gk.decode_split_plan(c, 1, 8193) == (48, 171)
