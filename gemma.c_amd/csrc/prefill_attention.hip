@@ -239,12 +239,14 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
   // A takes block j and the first x tiles of block J, workgroup B the other
   // T(J) - x, with x chosen so both get half. A split block's two halves
   // merge through the workspace.
+  // The (at most two) units are named values, not an array indexed by a
+  // runtime count, so they stay in registers (no scratch).
   struct Unit {
     int q0, t_lo, t_hi, slot, part;
   };
-  Unit units[2];
-  int n_units = 0;
   constexpr int kAllTiles = 1 << 30;
+  Unit unit0 = {0, 0, 0, -1, 0}, unit1 = {0, 0, 0, -1, 0};
+  int n_units = 0;
   if constexpr (kPaired) {
     const int rest = blockIdx.x / Hk;
     const int pair = rest >> 1, side = rest & 1;
@@ -254,30 +256,40 @@ __global__ __launch_bounds__(kPrefillThreads, 1) void prefill_chunk_kernel(Prefi
       return (prior + min(kPrefillRows * (blk + 1), Lq) - 1) / kTileKeys + 1;
     };
     if (j == J) {
-      if (side == 0) units[n_units++] = {kPrefillRows * j, 0, kAllTiles, -1, 0};
+      if (side == 0) {
+        unit0 = {kPrefillRows * j, 0, kAllTiles, -1, 0};
+        n_units = 1;
+      }
     } else if (j < J) {
       const int tj = tiles_of(j), tJ = tiles_of(J);
       int x = (tj + tJ) / 2 - tj;
       x = x < 0 ? 0 : (x > tJ ? tJ : x);
       const int slot = (b * Hk + head) * p.n_pairs + pair;
       if (side == 0) {
-        units[n_units++] = {kPrefillRows * j, 0, kAllTiles, -1, 0};
-        if (x > 0) units[n_units++] = {kPrefillRows * J, 0, x, x < tJ ? slot : -1, 0};
+        unit0 = {kPrefillRows * j, 0, kAllTiles, -1, 0};
+        n_units = 1;
+        if (x > 0) {
+          unit1 = {kPrefillRows * J, 0, x, x < tJ ? slot : -1, 0};
+          n_units = 2;
+        }
       } else if (x < tJ) {
-        units[n_units++] = {kPrefillRows * J, x, kAllTiles, x > 0 ? slot : -1, 1};
+        unit0 = {kPrefillRows * J, x, kAllTiles, x > 0 ? slot : -1, 1};
+        n_units = 1;
       }
     }
   } else {
-    units[n_units++] = {(int)(blockIdx.x / Hk) * kPrefillRows, 0, kAllTiles, -1, 0};
+    unit0 = {(int)(blockIdx.x / Hk) * kPrefillRows, 0, kAllTiles, -1, 0};
+    n_units = 1;
   }
   __shared__ int s_last;
 
   for (int u = 0; u < n_units; ++u) {
-  const int q0 = wave_uniform(units[u].q0);
-  const int unit_lo = wave_uniform(units[u].t_lo);
-  const int unit_hi = wave_uniform(units[u].t_hi);
-  const int unit_slot = wave_uniform(units[u].slot);
-  const int unit_part = wave_uniform(units[u].part);
+  const Unit &cur = u == 0 ? unit0 : unit1;
+  const int q0 = wave_uniform(cur.q0);
+  const int unit_lo = wave_uniform(cur.t_lo);
+  const int unit_hi = wave_uniform(cur.t_hi);
+  const int unit_slot = wave_uniform(cur.slot);
+  const int unit_part = wave_uniform(cur.part);
 
   // Rows of this lane: chunk row r = q0 + 16*wave + n % 16, q head 2*head + n / 16
   // (G = 2 for 16 query heads over 8 kv heads).
