@@ -121,6 +121,10 @@ def test_decode_outlier_keys_max_tracking(dev):
     (8, 256, 64, 0, 5000, 512, 10),
     (1, 512, 64, 0, 777, 64, 13),
     (8, 256, 1, 1024, 0, 32, 1),       # first token of a sequence
+    # Full rings are split by ring slot in a combining launch: the token's
+    # slot 1500 % 1024 = 476 is owned by a split in the middle, with page 16.
+    (8, 256, 16, 1024, 1500, 16, 64),
+    (8, 256, 1, 1024, 1023, 16, 64),   # the ring becomes full with this token
 ])
 def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, window,
                                                        seq_before, split_size, num_splits):
@@ -161,6 +165,38 @@ def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, wi
         assert np.abs(oracle.bf16_to_f32(again) - oracle.bf16_to_f32(got)).max() <= 2 ** -7
     assert not counters.cpu().numpy().any()
     assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
+
+
+@pytest.mark.parametrize("window,page", [(1024, 16), (0, 64)], ids=["ring", "global"])
+def test_fused_append_to_unmapped_page(dev, window, page):
+    """A token whose page is unmapped is not stored (the reference's write
+    rule) and does not attend; the other sequence's token does both. The
+    ring case is full, so its keys are split by ring slot."""
+    rng = np.random.default_rng(77 + page)
+    heads, dim = 8, 256
+    seq = [1601, 900]
+    batch = len(seq)
+    max_pages = ring_pages(window, page) if window else (max(seq) + page - 1) // page
+    cfg = cache_config(1, batch, page, max_pages, heads, dim, window)
+    pt = fill_page_table(cfg, seq)
+    pos = [n - 1 for n in seq]
+    pt[0 * max_pages + (pos[0] // page) % max_pages] = -1   # sequence 0's token page
+    n_rows = batch * max_pages * page
+    ck0 = randn_bf16(rng, (n_rows, heads, dim))
+    cv0 = randn_bf16(rng, (n_rows, heads, dim))
+    q = randn_bf16(rng, (batch, 16, dim))
+    k_new = randn_bf16(rng, (batch, heads, dim))
+    v_new = randn_bf16(rng, (batch, heads, dim))
+    exp_k, exp_v = ck0.copy(), cv0.copy()
+    oracle.kv_cache_write(exp_k, exp_v, cfg, pt, list(range(batch)), pos, 0, k_new, v_new)
+    exp = oracle.decode_attention(q, exp_k, exp_v, pt, seq, cfg, 0, 1 / 16)
+    split, n = gk.decode_split_plan(gk.make_config(*cfg), batch, max(seq))
+    ck, cv = to_dev(ck0, dev), to_dev(cv0, dev)
+    got = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, 1 / 16, split, n,
+                      fused=(pos, k_new, v_new))
+    assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
+    assert np.array_equal(from_dev_bf16(cv).reshape(exp_v.shape), exp_v)
+    assert_close(got, exp, "unmapped token page")
 
 
 D512_EDGES = [
