@@ -269,8 +269,10 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   // is requested first (one dependent round trip fewer before the first
   // tile); a ring that turns out not to be full refetches it by position.
   const int32_t ring_keys = c.max_pages_per_seq * c.page_size;
-  const int32_t key0 =
-      split * p.split_size + ((lane / Sh::KT) * key_lanes + key_lane) * Sh::KT + lane % Sh::KT;
+  // 64-bit: this load precedes the live-split check, and a split past the
+  // live ones may lie beyond int32 keys; the entry stays inside the row.
+  const int64_t key0 = (int64_t)split * p.split_size +
+                       ((lane / Sh::KT) * key_lanes + key_lane) * Sh::KT + lane % Sh::KT;
   // The per-sequence words the split depends on are all requested at once,
   // before anything waits: the length, the token position and the gate word
   // (an absent one reads the length's word and is ignored).
@@ -280,7 +282,8 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   const int32_t tok_word = *tok_src;
   const int32_t gate_word = *gate_src;
   const int32_t early_page = Sh::kStaged ? 0
-      : p.page_table[b * c.max_pages_per_seq + (key0 / c.page_size) % c.max_pages_per_seq];
+      : p.page_table[b * c.max_pages_per_seq +
+                     (int32_t)((key0 / c.page_size) % c.max_pages_per_seq)];
   const int32_t seq_len = wave_uniform(seq_word);
   const int32_t token_pos = p.token_position != nullptr ? wave_uniform(tok_word) : -1;
   int32_t first = c.window_size > 0 ? seq_len - c.window_size : 0;

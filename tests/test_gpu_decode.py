@@ -81,6 +81,33 @@ def test_decode_matches_oracle(dev, heads, dim, page, window, seq, split_size, n
             assert not got[b].any()
 
 
+def test_decode_huge_split_size(dev):
+    """Splits past the live ones with split * split_size beyond int32: only
+    split 0 holds keys, the others exit; the fused append lands and the output
+    equals the oracle's."""
+    rng = np.random.default_rng(21)
+    heads, dim, page, window = 8, 256, 1, 1024
+    seq = [1500]
+    cfg = cache_config(1, 1, page, ring_pages(window, page), heads, dim, window)
+    pt = fill_page_table(cfg, seq)
+    rows = ring_pages(window, page) * page
+    ck0 = randn_bf16(rng, (rows, heads, dim))
+    cv0 = randn_bf16(rng, (rows, heads, dim))
+    q = randn_bf16(rng, (1, 16, dim))
+    k_new = randn_bf16(rng, (1, heads, dim))
+    v_new = randn_bf16(rng, (1, heads, dim))
+    pos = [seq[0] - 1]
+    exp_k, exp_v = ck0.copy(), cv0.copy()
+    oracle.kv_cache_write(exp_k, exp_v, cfg, pt, [0], pos, 0, k_new, v_new)
+    exp = oracle.decode_attention(q, exp_k, exp_v, pt, seq, cfg, 0, 1 / 16)
+    ck, cv = to_dev(ck0, dev), to_dev(cv0, dev)
+    split_size, num_splits = 1 << 30, 8   # split 7 starts at 7 * 2^30 keys
+    got = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, 1 / 16, split_size, num_splits,
+                      fused=(pos, k_new, v_new))
+    assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k)
+    assert_close(got, exp, "huge split size")
+
+
 def test_decode_skips_unmapped_pages(dev):
     rng = np.random.default_rng(11)
     heads, dim, page = 8, 256, 16
