@@ -148,9 +148,11 @@ def test_decode_outlier_keys_max_tracking(dev):
     (8, 256, 64, 0, 5000, 512, 10),
     (1, 512, 64, 0, 777, 64, 13),
     (8, 256, 1, 1024, 0, 32, 1),       # first token of a sequence
-    # Full rings are split by ring slot in a combining launch: the token's
-    # slot 1500 % 1024 = 476 is owned by a split in the middle, with page 16.
-    (8, 256, 16, 1024, 1500, 16, 64),
+    # Full rings are split by ring slot in a combining launch. A ring whose
+    # slots are exactly the window (page 16 x 64 pages here; ring_pages adds a
+    # page for page sizes above 1) is full from 1024 keys on: the token's
+    # slot 1500 % 1024 = 476 is owned by a split in the middle.
+    (8, 256, -16, 1024, 1500, 16, 64),
     (8, 256, 1, 1024, 1023, 16, 64),   # the ring becomes full with this token
 ])
 def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, window,
@@ -158,7 +160,10 @@ def test_fused_append_decode_equals_append_then_attend(dev, heads, dim, page, wi
     rng = np.random.default_rng(seq_before + 3)
     batch = 2
     seq = [seq_before + 1, max(1, seq_before // 3 + 1)]
-    max_pages = ring_pages(window, page) if window else (max(seq) + page - 1) // page
+    exact_ring = page < 0   # a negative page size asks for a ring of exactly the window
+    page = abs(page)
+    max_pages = (window // page if exact_ring else ring_pages(window, page)) if window else \
+        (max(seq) + page - 1) // page
     cfg = cache_config(1, batch, page, max_pages, heads, dim, window)
     pt = fill_page_table(cfg, seq)
     n_rows = batch * max_pages * page
@@ -415,3 +420,70 @@ def test_split_and_combine_phases(dev, heads, dim, page, window, seq, split_size
     assert np.array_equal(two_phase, one_call)
     exp = oracle.decode_combine(om, ol, oa, seq, cfg, split_size, num_splits)
     assert_close(two_phase, exp, "combine of oracle partials")
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_decode_randomized_against_oracle(dev, seed):
+    """Seeded random cases against the oracle: geometry, cache kind (ring
+    with a spare page, ring of exactly the window -- full rings are split by
+    ring slot --, global), page size, batch, ragged lengths including 0 and
+    the window edges, planned or arbitrary split sizes, fused append or
+    not, separate or in-kernel combine. Appends bit-exact, outputs within
+    the north-star tolerance."""
+    import torch
+    rng = np.random.default_rng(4000 + seed)
+    heads, dim = (8, 256) if rng.random() < 0.75 else (1, 512)
+    kind = ["ring", "exact_ring", "global"][int(rng.integers(0, 3))]
+    batch = int(rng.integers(1, 4))
+    if kind == "global":
+        page = int(rng.choice([16, 64]))
+        window = 0
+        seq = [int(rng.integers(0, 3000)) for _ in range(batch)]
+        max_pages = (max(max(seq), 1) + 1 + page - 1) // page
+    else:
+        window = int(rng.choice([64, 256, 1024]))
+        page = int(rng.choice([1, 4, 16]))
+        edges = [0, 1, window - 1, window, window + 1, 2 * window + 5]
+        seq = [int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(0, 3 * window))
+               for _ in range(batch)]
+        max_pages = window // page if kind == "exact_ring" else ring_pages(window, page)
+    fused = rng.random() < 0.7
+    if fused:
+        seq = [n + 1 for n in seq]   # the appended token is the last live key
+    cfg = cache_config(1, batch, page, max_pages, heads, dim, window)
+    pt = fill_page_table(cfg, seq)
+    n_rows = batch * max_pages * page
+    ck0 = randn_bf16(rng, (n_rows, heads, dim))
+    cv0 = randn_bf16(rng, (n_rows, heads, dim))
+    q = randn_bf16(rng, (batch, 16, dim))
+    scale = 1.0 / math.sqrt(dim)
+    live = max(min(n, window) if window else n for n in seq)
+    if rng.random() < 0.5:
+        split_size, num_splits = gk.decode_split_plan(gk.make_config(*cfg), batch, max(live, 1))
+    else:
+        split_size = int(rng.choice([16, 20, 48, 96, 333]))
+        num_splits = max(1, (live + split_size - 1) // split_size)
+    exp_k, exp_v = ck0.copy(), cv0.copy()
+    fused_args = None
+    if fused:
+        k_new = randn_bf16(rng, (batch, heads, dim))
+        v_new = randn_bf16(rng, (batch, heads, dim))
+        pos = [n - 1 for n in seq]
+        oracle.kv_cache_write(exp_k, exp_v, cfg, pt, list(range(batch)), pos, 0, k_new, v_new)
+        fused_args = (pos, k_new, v_new)
+    exp = oracle.decode_attention(q, exp_k, exp_v, pt, seq, cfg, 0, scale)
+    counters = None
+    if fused and num_splits > 1 and rng.random() < 0.3:
+        counters = torch.zeros(batch * heads, dtype=torch.int32, device=dev)
+    what = (f"seed {seed}: {heads}x{dim} {kind} page {page} window {window} seq {seq} "
+            f"split {split_size}x{num_splits} fused {fused} counters {counters is not None}")
+    print(what, flush=True)
+    ck, cv = to_dev(ck0, dev), to_dev(cv0, dev)
+    got = _run_decode(dev, cfg, q, ck, cv, pt, seq, 0, scale, split_size, num_splits,
+                      fused=fused_args, counters=counters)
+    assert np.array_equal(from_dev_bf16(ck).reshape(exp_k.shape), exp_k), what
+    assert np.array_equal(from_dev_bf16(cv).reshape(exp_v.shape), exp_v), what
+    assert_close(got, exp, what)
+    for b, n in enumerate(seq):
+        if n == 0:
+            assert not got[b].any(), what
