@@ -222,6 +222,73 @@ __device__ __forceinline__ uint4 prep_pack(uint4 raw, const uint16_t *weight,
                     pack_bf16x2(y[6], y[7]));
 }
 
+// The inputs prep_pack reads besides the row, loaded ahead of the math: the
+// lane's 8 weights (packed bf16) and cos / sin of its rotary pair.
+struct PrepInputs {
+  uint4 w;
+  float4 c0, c1, s0, s1;
+};
+template <int LPR, int kRot>
+__device__ __forceinline__ PrepInputs prep_inputs(const uint16_t *weight, const float *cos_row,
+                                                  const float *sin_row, int cpack) {
+  PrepInputs in;
+  in.w = weight != nullptr ? load128(weight + cpack * kPackElems) : make_uint4(0, 0, 0, 0);
+  const int d0 = cpack * kPackElems;
+  const int pair = d0 < kRot / 2 ? d0 : d0 - kRot / 2;
+  const bool rot = weight != nullptr && d0 < kRot;
+  // Scalar loads: the tables come through the C-ABI with no alignment promise.
+  const float *cr = rot ? cos_row + pair : nullptr;
+  const float *sr = rot ? sin_row + pair : nullptr;
+  in.c0 = rot ? make_float4(cr[0], cr[1], cr[2], cr[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  in.c1 = rot ? make_float4(cr[4], cr[5], cr[6], cr[7]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  in.s0 = rot ? make_float4(sr[0], sr[1], sr[2], sr[3]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  in.s1 = rot ? make_float4(sr[4], sr[5], sr[6], sr[7]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  return in;
+}
+// prep_pack's arithmetic on preloaded inputs (weighted: learned RMSNorm +
+// RoPE; otherwise the scale-free RMSNorm), the same operations in the same
+// order.
+template <int LPR, int kRot>
+__device__ __forceinline__ uint4 prep_math(uint4 raw, bool weighted, const PrepInputs &in,
+                                           int cpack) {
+  float x[8];
+  unpack8(raw, x);
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
+  ss += lane_xor<1>(ss);
+  ss += lane_xor<2>(ss);
+  ss += lane_xor<4>(ss);
+  ss += lane_xor<8>(ss);
+  ss = xor_sum<16>(ss);
+  if constexpr (LPR == 64) ss = xor_sum<32>(ss);
+  const float scale = 1.0f / sqrtf(ss / (float)(LPR * kPackElems) + kRmsEps);
+  float y[8];
+  if (!weighted) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = x[i] * scale;
+  } else {
+    float w[8];
+    unpack8(in.w, w);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) y[i] = x[i] * scale * w[i];
+    constexpr int kHalf = kRot / 2;
+    float partner[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) partner[i] = lane_xor<kHalf / kPackElems>(y[i]);
+    const int d0 = cpack * kPackElems;
+    if (d0 < kRot) {
+      const float sign = d0 < kHalf ? -1.0f : 1.0f;
+      const float c[8] = {in.c0.x, in.c0.y, in.c0.z, in.c0.w, in.c1.x, in.c1.y, in.c1.z, in.c1.w};
+      const float sn[8] = {in.s0.x, in.s0.y, in.s0.z, in.s0.w, in.s1.x, in.s1.y, in.s1.z, in.s1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = fmaf(sign * partner[i], sn[i], y[i] * c[i]);
+    }
+  }
+  return make_uint4(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]), pack_bf16x2(y[4], y[5]),
+                    pack_bf16x2(y[6], y[7]));
+}
+
 template <class Sh>
 __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeParams p) {
   constexpr int G = Sh::G, GW = Sh::GW, HG = Sh::HG, LPR = Sh::LPR, RPL = Sh::RPL;
@@ -409,23 +476,36 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   uint32_t qw[GW][4];
   // With fused preparation q is normalised and rotated here, at the token's
   // position (a sequence without a token this step uses q as given).
-  // Loaded after the first tile's loads are issued: memory loads complete
-  // in order, so a q load ahead of them would hold up the page lookup they
-  // wait for.
+  // Memory loads complete in order. Without preparation q is loaded after
+  // the first tile's loads are issued (ahead of them it would hold up the
+  // page lookup they wait for); with preparation its loads and the norm
+  // weights and RoPE rows go out before the tile loads (q_issue) and the
+  // arithmetic runs while the tiles are in flight (q_finish).
   const bool prep_q = prep && token_pos >= 0;
   const int32_t q_pos = prep_q ? token_pos : 0;
-  auto load_q = [&]() __attribute__((always_inline)) {
+  uint4 q_raw[GW];
+  PrepInputs q_in{};
+  auto q_issue = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < GW; ++g) {
       const int qh = head * G + hg * GW + g;
-      uint4 qp = load128(p.q + ((int64_t)b * kQueryHeads + qh) * D + cpack * kPackElems);
-      if (prep_q) {
-        qp = prep_pack<LPR, Sh::kRot>(qp, p.q_norm_weight,
-                                      p.cos + (int64_t)q_pos * (Sh::kRot / 2),
-                                      p.sin + (int64_t)q_pos * (Sh::kRot / 2), cpack);
-      }
+      q_raw[g] = load128(p.q + ((int64_t)b * kQueryHeads + qh) * D + cpack * kPackElems);
+    }
+    if (prep_q) {
+      q_in = prep_inputs<LPR, Sh::kRot>(p.q_norm_weight, p.cos + (int64_t)q_pos * (Sh::kRot / 2),
+                                        p.sin + (int64_t)q_pos * (Sh::kRot / 2), cpack);
+    }
+  };
+  auto q_finish = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int g = 0; g < GW; ++g) {
+      const uint4 qp = prep_q ? prep_math<LPR, Sh::kRot>(q_raw[g], true, q_in, cpack) : q_raw[g];
       qw[g][0] = qp.x; qw[g][1] = qp.y; qw[g][2] = qp.z; qw[g][3] = qp.w;
     }
+  };
+  auto load_q = [&]() __attribute__((always_inline)) {
+    q_issue();
+    q_finish();
   };
 
   // Score-lane identity after the butterfly: one (key, head) per lane.
@@ -696,11 +776,13 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
     // A wave with one or two tiles (the sliding layers' short splits) runs
     // them straight: the pipeline below would also issue the loads of the
     // dead tiles up to the end of the chunk and wait for them before exit.
+    if (prep) q_issue();
     publish(0, page_row(0, early_ok ? early_page : fetch_page(0)));
     SPLIT_MARK(2);
     TileBuf buf0, buf1;
     issue(buf0, 0, 0);
-    load_q();
+    if (!prep) q_issue();
+    q_finish();
     if (my_tiles == 2) {
       issue(buf1, 0, 1);
       compute(buf0);
@@ -717,12 +799,14 @@ __global__ __launch_bounds__(Sh::kMaxW * kWave) void decode_split_kernel(DecodeP
   // flight for a whole chunk. Every load is issued on every path, so the
   // memory wait counters stay exact.
   static_assert(CT % 2 == 0, "tiles per chunk alternate between two buffers");
+    if (prep) q_issue();
     publish(0, page_row(0, early_ok ? early_page : fetch_page(0)));
     SPLIT_MARK(2);
     int32_t next_page = fetch_page(1);
     TileBuf buf0, buf1;
     issue(buf0, 0, 0);
-    load_q();
+    if (!prep) q_issue();
+    q_finish();
     for (int32_t m = 0; m < my_chunks; ++m) {
 #pragma unroll
       for (int t = 0; t < CT; t += 2) {
